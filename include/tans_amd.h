@@ -1,0 +1,143 @@
+/*
+ * tans_amd.h -- C ABI of the MI355X (gfx950) fused tANS FP8 library.
+ *
+ * One shared library, libtans_amd.so, holds the CPU encoder and the HIP
+ * kernels.  Every entry point takes plain pointers and sizes; device
+ * pointers are HIP device memory, `stream` is a hipStream_t (NULL = the
+ * null stream).  Launches are asynchronous on `stream`; the return code
+ * covers argument validation and the launch itself.  All functions return
+ * TANS_OK (0) or a negative TANS_E* code; tans_last_error() gives a message
+ * for the calling thread's last failure.
+ *
+ * Data format ("wave64 lane layout"):
+ *   - The input is K lanes (rows) of N FP8 E4M3FN bytes.  A lane is one tANS
+ *     state sequence; 64 consecutive lanes form a group, decoded by one
+ *     wave64 (lane j of the group = wave lane j).
+ *   - Symbols: the exponent nibble e = (b >> 3) & 15.  Pair alphabet: one
+ *     symbol e0*16+e1 per two elements, table of 2^12 states.  Nibble
+ *     alphabet: one symbol per element, 2^11 states.  The table size fixes
+ *     the alphabet.
+ *   - Bitstream: each lane's bits, in decode order, are cut into u32 words
+ *     read LSB first; every decode step reads nb bits as one value.  The
+ *     words of the 64 lanes of group g form one stream at
+ *     comp_words[offsets[g] ..], ordered by the refill schedule all decoders
+ *     follow: each lane starts with an empty buffer; before every second
+ *     step (steps 0, 2, 4, ...) each active lane holding fewer than 24 bits
+ *     takes the next stream word (lanes in ascending order) and gains 32
+ *     bits.  Streams start on 16-byte boundaries; 1 KiB of zero words
+ *     follows the last one.  offsets is int64 [n_groups + 1], in words.
+ *   - states[k] is lane k's initial decoder state in [L, 2L).
+ *   - Sign/mantissa nibbles: 16-element tiles, 8 bytes per (tile, lane) at
+ *     sm[(t * K + k) * 8]; u32 word h covers elements 8h..8h+7 as
+ *     (A & 0x87878787) | rotl(B & 0x87878787, 4), A/B being elements
+ *     8h..8h+3 / 8h+4..8h+7 read as little-endian words.
+ *   - Decode table: L entries of two u32 words:
+ *       word0 = nb | (e0 << 11) | (e1 << 19)   (nibble alphabet: nb | e << 11)
+ *       word1 = (base - L) * 8
+ *     for the state x = L + slot, with x_prev = f_sym + rank,
+ *     nb = doublings of x_prev until >= L, base = x_prev << nb.
+ */
+#ifndef TANS_AMD_H
+#define TANS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TANS_OK = 0,
+    TANS_EINVAL = -1,     /* bad argument (shape, size, null pointer)      */
+    TANS_ENOMEM = -2,     /* host allocation failed                          */
+    TANS_ESYMBOL = -3,    /* data holds a symbol whose frequency is 0         */
+    TANS_ETABLE = -4,     /* freqs / spread inconsistent                     */
+    TANS_EHIP = -5        /* a HIP runtime call failed                       */
+};
+
+#define TANS_LANES 64          /* lanes per group (one wave64)             */
+#define TANS_TILE 16           /* elements per lane per tile                */
+#define TANS_PAIR_LOG2L 12     /* table size of the pair alphabet          */
+#define TANS_NIBBLE_LOG2L 11   /* table size of the nibble alphabet        */
+
+/* Message for the calling thread's last failure ("" if none). */
+const char* tans_last_error(void);
+
+/* ---------------- CPU side ------------------------------------------- */
+
+/* Split FP8 bytes into tANS symbols and packed sign/mantissa nibbles.
+ * Replaces the nibble split / pair forming / sm packing of
+ * rans_vectoradd/tans_codec.py:109-124.
+ *   fp8      [K, N] bytes, N even
+ *   sps      2 = pair alphabet (symbols [K, N/2]), 1 = nibble ([K, N])
+ *   symbols  output, K*N/2 bytes (pair) or K*N bytes (nibble)
+ *   sm       output, ceil(N/16) * K * 8 bytes (layout above)            */
+int tans_split_fp8(const uint8_t* fp8, int64_t K, int64_t N, int32_t sps,
+                   uint8_t* symbols, uint8_t* sm);
+
+/* Host decode table from (spread, freqs).  Replaces
+ * rans_vectoradd/tans_codec.py:63-87 and csrc/tans_decode.cu:23-59.
+ *   spread [2^log2L] slot -> symbol; freqs [nsym], nsym 256 (pair, log2L
+ *   12) or 16 (nibble, log2L 11); table output [2^log2L * 2] u32.       */
+int tans_build_decode_table(const int32_t* spread, const int32_t* freqs,
+                            int32_t nsym, int32_t log2L, uint32_t* table);
+
+/* CPU encoder into the wave64 lane layout.  Together these replace
+ * tans_encode_interleaved, csrc/tans_codec.cpp:69-196.
+ * begin: encodes symbols [K, S] (S symbols per lane) with the table given
+ *   by freqs [nsym] (summing to 2^log2L) and spread [2^log2L]; reports the
+ *   output sizes.  finish: writes comp [comp_bytes], states [K] and
+ *   offsets [n_offsets] and releases the handle.  free: releases a handle
+ *   without writing (after an error).                                   */
+int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S,
+                      const int32_t* freqs, int32_t nsym, const int32_t* spread,
+                      int32_t log2L, void** handle, int64_t* comp_bytes,
+                      int64_t* n_offsets);
+int tans_encode_finish(void* handle, uint8_t* comp, uint16_t* states,
+                       int64_t* offsets);
+void tans_encode_free(void* handle);
+
+/* ---------------- GPU side (gfx950) ---------------------------------- */
+
+/* C = A, 16-byte vectors; n % 16 == 0.  Replaces fp8_memcpy,
+ * csrc/fp8_memcpy.cu:45-64 (the HBM-ceiling kernel).                   */
+int tans_fp8_memcpy(const void* a, void* c, int64_t n, void* stream);
+
+/* C[i] = fp8_e4m3(float(A[i]) + float(B[i])), round-to-nearest-even with
+ * saturation to +-448; n % 16 == 0.  Replaces fp8_vecadd_raw,
+ * csrc/vecadd.cu:268-288.                                              */
+int tans_fp8_vecadd_raw(const void* a, const void* b, void* c, int64_t n,
+                        void* stream);
+
+/* Device decode table from device spread/freqs (no host round trip).
+ * Same output as tans_build_decode_table.                               */
+int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs,
+                                   int32_t nsym, int32_t log2L, uint32_t* table,
+                                   void* stream);
+
+/* Fused decode of two encodings (same table) + FP8 add.
+ * out is tiled [N/16, K, 16]: out[(t*K + k)*16 + i] = element 16t+i of
+ * lane k.  N % 16 == 0.  comp_bytes_* bound the reads: malformed offsets
+ * cannot make a kernel read outside the buffers.  Replaces
+ * fp8_vecadd_fused_tans, csrc/vecadd.cu:290-393.                        */
+int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes,
+                          const int64_t* a_offsets, const uint16_t* a_states,
+                          const void* a_sm,
+                          const void* b_comp, int64_t b_comp_bytes,
+                          const int64_t* b_offsets, const uint16_t* b_states,
+                          const void* b_sm,
+                          const uint32_t* table, int32_t log2L,
+                          int64_t K, int64_t N, void* out, void* stream);
+
+/* Standalone decode to FP8 bytes, out [N, K] (element-major, lane-minor).
+ * N even.  Replaces gpu_tans_decode, csrc/tans_decode.cu:159-210.       */
+int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
+                const uint16_t* states, const void* sm,
+                const uint32_t* table, int32_t log2L,
+                int64_t K, int64_t N, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TANS_AMD_H */

@@ -1,0 +1,297 @@
+// CPU side of the MI355X tANS FP8 library: nibble split, decode-table
+// construction and the encoder into the wave64 lane layout (format described
+// in include/tans_amd.h).
+//
+// The encoder follows the tANS construction of csrc/tans_codec.cpp:22-60
+// (walk the symbols backwards from x = L, renormalise the state into
+// [f_s, 2 f_s) by emitting its low bits, then x = L + slot of the
+// rank-th occurrence of s in the spread, tans_codec.cpp:100-118).  What
+// differs is the bit order and layout: the bits of each step are kept as one
+// chunk, the chunks are written forwards in decode order LSB-first, and the
+// lanes of a 64-lane group are interleaved word by word in rows, so a wave's
+// refills hit a few adjacent 256-byte rows.  There is no partial-slab count:
+// a lane's bitstream starts at bit 0 of its first word.
+#include "../../include/tans_amd.h"
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* msg) {
+    g_err = msg;
+    return code;
+}
+
+inline uint32_t rotl32(uint32_t v, int r) { return (v << r) | (v >> (32 - r)); }
+
+inline int ilog2(uint32_t v) { return 31 - __builtin_clz(v); }
+
+// Refill schedule shared with the decoders: before every second step a lane
+// whose buffer holds fewer than kRefillBelow bits takes the next 32-bit word
+// of its group's stream (lanes in ascending order).  Two steps read at most
+// 2*12 bits, so the buffer never runs dry and never exceeds 64 bits.
+constexpr int kRefillBelow = 24;
+// Zero words appended after the last group, so 16-byte segment loads near
+// the end stay inside the buffer.
+constexpr int64_t kTailWords = 256;
+
+struct EncTables {
+    std::vector<uint32_t> start;   // start[s]: first index of s in next
+    std::vector<uint32_t> next;    // next[start[s] + rank] = L + slot
+    std::vector<uint32_t> freq;
+};
+
+int build_enc_tables(const int32_t* freqs, int32_t nsym, const int32_t* spread,
+                     int32_t log2L, EncTables& t) {
+    const uint32_t L = 1u << log2L;
+    t.start.assign(nsym, 0);
+    t.freq.assign(nsym, 0);
+    t.next.assign(L, 0);
+    uint64_t sum = 0;
+    for (int s = 0; s < nsym; s++) {
+        if (freqs[s] < 0) return fail(TANS_ETABLE, "negative frequency");
+        t.start[s] = (uint32_t)sum;
+        t.freq[s] = (uint32_t)freqs[s];
+        sum += (uint32_t)freqs[s];
+    }
+    if (sum != L) return fail(TANS_ETABLE, "freqs must sum to L = 2^log2L");
+    std::vector<uint32_t> cnt(nsym, 0);
+    for (uint32_t slot = 0; slot < L; slot++) {
+        int s = spread[slot];
+        if (s < 0 || s >= nsym) return fail(TANS_ETABLE, "spread symbol out of range");
+        if (cnt[s] >= t.freq[s]) return fail(TANS_ETABLE, "spread disagrees with freqs");
+        t.next[t.start[s] + cnt[s]++] = L + slot;
+    }
+    return TANS_OK;
+}
+
+// Encode one lane of S symbols.  chunk[i] receives step i's bits (low 16)
+// and nb (bits 16+).  words receives the decode-order bitstream, LSB first
+// (room for ceil(S*log2L/32)+1 words).  Returns the word count, or -1 if a
+// symbol has frequency 0.
+int64_t encode_lane(const uint8_t* sym, int64_t S, const EncTables& t, uint32_t L,
+                    uint32_t* chunk, uint32_t* words, uint32_t* x0) {
+    uint32_t x = L;
+    const uint32_t* freq = t.freq.data();
+    const uint32_t* start = t.start.data();
+    const uint32_t* next = t.next.data();
+    for (int64_t i = S - 1; i >= 0; i--) {
+        const uint32_t s = sym[i];
+        const uint32_t f = freq[s];
+        if (f == 0) return -1;
+        // nb such that (x >> nb) lies in [f, 2f)
+        int nb = ilog2(x) - ilog2(f);
+        if ((x >> nb) < f) nb--;
+        chunk[i] = (x & ((1u << nb) - 1u)) | ((uint32_t)nb << 16);
+        x = next[start[s] + (x >> nb) - f];
+    }
+    *x0 = x;
+    uint64_t acc = 0;
+    int n = 0;
+    int64_t nw = 0;
+    for (int64_t i = 0; i < S; i++) {
+        acc |= (uint64_t)(chunk[i] & 0xFFFFu) << n;
+        n += (int)(chunk[i] >> 16);
+        if (n >= 32) {
+            words[nw++] = (uint32_t)acc;
+            acc >>= 32;
+            n -= 32;
+        }
+    }
+    if (n > 0) words[nw++] = (uint32_t)acc;
+    return nw;
+}
+
+struct EncodeHandle {
+    int64_t K = 0, S = 0, n_groups = 0, total_words = 0;
+    std::vector<std::vector<uint32_t>> streams;   // per group, 4-word padded
+    std::vector<uint16_t> states;
+};
+
+}  // namespace
+
+extern "C" {
+
+const char* tans_last_error(void) { return g_err.c_str(); }
+
+void tans_internal_set_error(const char* msg) { g_err = msg ? msg : ""; }
+
+int tans_split_fp8(const uint8_t* fp8, int64_t K, int64_t N, int32_t sps,
+                   uint8_t* symbols, uint8_t* sm) {
+    if ((!fp8 && K * N != 0) || K < 0 || N < 0 || (N % 2) != 0)
+        return fail(TANS_EINVAL, "split: need K >= 0 and even N >= 0");
+    if (sps != 1 && sps != 2) return fail(TANS_EINVAL, "split: sps must be 1 or 2");
+    const int64_t S = N / sps;
+    const int64_t n_tiles = (N + TANS_TILE - 1) / TANS_TILE;
+    #pragma omp parallel for schedule(static)
+    for (int64_t k = 0; k < K; k++) {
+        const uint8_t* row = fp8 + k * N;
+        uint8_t* srow = symbols + k * S;
+        if (sps == 2) {
+            for (int64_t i = 0; i < S; i++)
+                srow[i] = (uint8_t)((((row[2 * i] >> 3) & 0xF) << 4) | ((row[2 * i + 1] >> 3) & 0xF));
+        } else {
+            for (int64_t i = 0; i < S; i++) srow[i] = (uint8_t)((row[i] >> 3) & 0xF);
+        }
+        for (int64_t t = 0; t < n_tiles; t++) {
+            uint8_t tile[TANS_TILE] = {0};
+            int64_t m = std::min<int64_t>(TANS_TILE, N - t * TANS_TILE);
+            std::memcpy(tile, row + t * TANS_TILE, (size_t)m);
+            uint32_t w[2];
+            for (int h = 0; h < 2; h++) {
+                uint32_t a, b;
+                std::memcpy(&a, tile + 8 * h, 4);
+                std::memcpy(&b, tile + 8 * h + 4, 4);
+                w[h] = (a & 0x87878787u) | rotl32(b & 0x87878787u, 4);
+            }
+            std::memcpy(sm + (t * K + k) * 8, w, 8);
+        }
+    }
+    return TANS_OK;
+}
+
+int tans_build_decode_table(const int32_t* spread, const int32_t* freqs, int32_t nsym,
+                            int32_t log2L, uint32_t* table) {
+    if (!spread || !freqs || !table) return fail(TANS_EINVAL, "table: null pointer");
+    if (!((nsym == 256 && log2L == TANS_PAIR_LOG2L) || (nsym == 16 && log2L == TANS_NIBBLE_LOG2L)))
+        return fail(TANS_EINVAL, "table: need (nsym 256, log2L 12) or (nsym 16, log2L 11)");
+    EncTables t;
+    int rc = build_enc_tables(freqs, nsym, spread, log2L, t);   // validates
+    if (rc) return rc;
+    const uint32_t L = 1u << log2L;
+    std::vector<uint32_t> cnt(nsym, 0);
+    for (uint32_t slot = 0; slot < L; slot++) {
+        const uint32_t s = (uint32_t)spread[slot];
+        const uint32_t xp = t.freq[s] + cnt[s]++;
+        const int nb = log2L - ilog2(xp);
+        const uint32_t base = xp << nb;
+        const uint32_t ex = (nsym == 256) ? (((s >> 4) << 11) | ((s & 0xF) << 19)) : (s << 11);
+        table[2 * slot] = (uint32_t)nb | ex;
+        table[2 * slot + 1] = (base - L) * 8u;
+    }
+    return TANS_OK;
+}
+
+int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_t* freqs,
+                      int32_t nsym, const int32_t* spread, int32_t log2L, void** handle,
+                      int64_t* comp_bytes, int64_t* n_offsets) {
+    if (!handle || !comp_bytes || !n_offsets) return fail(TANS_EINVAL, "encode: null output");
+    *handle = nullptr;
+    if (K < 0 || S < 0 || (!symbols && K * S != 0) || !freqs || !spread)
+        return fail(TANS_EINVAL, "encode: bad shape or null input");
+    if (log2L < 1 || log2L > 12) return fail(TANS_EINVAL, "encode: log2L must be in [1, 12]");
+    if (nsym < 1 || nsym > 256) return fail(TANS_EINVAL, "encode: nsym must be in [1, 256]");
+    EncTables t;
+    int rc = build_enc_tables(freqs, nsym, spread, log2L, t);
+    if (rc) return rc;
+    const uint32_t L = 1u << log2L;
+    EncodeHandle* h = new (std::nothrow) EncodeHandle;
+    if (!h) return fail(TANS_ENOMEM, "encode: out of memory");
+    h->K = K;
+    h->S = S;
+    h->n_groups = (K + TANS_LANES - 1) / TANS_LANES;
+    try {
+        h->streams.resize((size_t)h->n_groups);
+        h->states.assign((size_t)K, 0);
+    } catch (...) {
+        delete h;
+        return fail(TANS_ENOMEM, "encode: out of memory");
+    }
+    const int64_t max_words = (S * (int64_t)log2L + 31) / 32 + 1;
+    const int64_t n_checks = (S + 1) / 2;
+    int bad_symbol = 0;
+    #pragma omp parallel
+    {
+        std::vector<uint32_t> chunk((size_t)std::max<int64_t>(S, 1) * TANS_LANES);
+        std::vector<uint32_t> words((size_t)(TANS_LANES * max_words));
+        std::vector<int64_t> nw(TANS_LANES), taken(TANS_LANES);
+        std::vector<int32_t> cnt(TANS_LANES);
+        #pragma omp for schedule(dynamic, 4)
+        for (int64_t g = 0; g < h->n_groups; g++) {
+            const int lanes = (int)std::min<int64_t>(TANS_LANES, K - g * TANS_LANES);
+            bool ok = true;
+            for (int j = 0; j < lanes; j++) {
+                const int64_t k = g * TANS_LANES + j;
+                uint32_t x0;
+                nw[j] = encode_lane(symbols + k * S, S, t, L, chunk.data() + j * S,
+                                    words.data() + j * max_words, &x0);
+                if (nw[j] < 0) { ok = false; break; }
+                h->states[(size_t)k] = (uint16_t)x0;
+            }
+            if (!ok) {
+                #pragma omp atomic write
+                bad_symbol = 1;
+                continue;
+            }
+            // Replay the decoders' refill schedule to order the words.
+            std::vector<uint32_t>& out = h->streams[(size_t)g];
+            out.clear();
+            out.reserve((size_t)(lanes * (max_words + 2)));
+            for (int j = 0; j < lanes; j++) { cnt[j] = 0; taken[j] = 0; }
+            for (int64_t q = 0; q < n_checks; q++) {
+                for (int j = 0; j < lanes; j++) {
+                    if (cnt[j] < kRefillBelow) {
+                        const int64_t r = taken[j]++;
+                        out.push_back(r < nw[j] ? words[(size_t)(j * max_words + r)] : 0u);
+                        cnt[j] += 32;
+                    }
+                    const uint32_t* ch = chunk.data() + j * S;
+                    cnt[j] -= (int32_t)(ch[2 * q] >> 16);
+                    if (2 * q + 1 < S) cnt[j] -= (int32_t)(ch[2 * q + 1] >> 16);
+                }
+            }
+            while (out.size() % 4) out.push_back(0u);
+        }
+    }
+    if (bad_symbol) {
+        delete h;
+        return fail(TANS_ESYMBOL, "encode: data holds a symbol whose frequency is 0");
+    }
+    int64_t total = 0;
+    for (const auto& st : h->streams) total += (int64_t)st.size();
+    h->total_words = total;
+    *comp_bytes = (total + kTailWords) * 4;
+    *n_offsets = h->n_groups + 1;
+    *handle = h;
+    return TANS_OK;
+}
+
+int tans_encode_finish(void* handle, uint8_t* comp, uint16_t* states, int64_t* offsets) {
+    EncodeHandle* h = static_cast<EncodeHandle*>(handle);
+    if (!h || !comp || !offsets || (!states && h->K)) {
+        delete h;
+        return fail(TANS_EINVAL, "encode_finish: null argument");
+    }
+    int64_t cum = 0;
+    for (int64_t g = 0; g < h->n_groups; g++) {
+        offsets[g] = cum;
+        cum += (int64_t)h->streams[(size_t)g].size();
+    }
+    offsets[h->n_groups] = cum;
+    uint32_t* c32 = reinterpret_cast<uint32_t*>(comp);
+    #pragma omp parallel for schedule(static)
+    for (int64_t g = 0; g < h->n_groups; g++) {
+        const auto& st = h->streams[(size_t)g];
+        if (!st.empty()) std::memcpy(c32 + offsets[g], st.data(), st.size() * 4);
+    }
+    std::memset(c32 + cum, 0, (size_t)kTailWords * 4);
+    if (h->K) std::memcpy(states, h->states.data(), (size_t)h->K * 2);
+    delete h;
+    return TANS_OK;
+}
+
+void tans_encode_free(void* handle) { delete static_cast<EncodeHandle*>(handle); }
+
+}  // extern "C"

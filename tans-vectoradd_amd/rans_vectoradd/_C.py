@@ -1,0 +1,208 @@
+"""Drop-in for the reference's pybind11 module ``rans_vectoradd._C``
+(csrc/fp8_memcpy.cu:66-78): the same five functions, positional arguments
+and return shapes, implemented over the C ABI of libtans_amd.so.
+
+Differences from the reference, all inside the tensors the encoder returns:
+
+* ``offsets`` are int64 word offsets of each 64-lane group's stream (the
+  reference: int32 byte offsets of 128-stream blocks);
+* ``partial_cnts`` is empty: the layout has no partial slabs; it is accepted
+  and ignored by the decoders, as any tensor would be;
+* ``decode_tbl`` holds 2 int32 words per state (build_decode_table);
+* the sign/mantissa tensor uses the 16-element tile layout of
+  include/tans_amd.h for both the fused and the standalone decoder.
+
+Validation mirrors the reference's TORCH_CHECKs and raises RuntimeError.
+Kernels run on the current torch stream of the inputs' device.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._lib import (TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PAIR_LOG2L, TANS_TILE, check,
+                   lib)
+
+__all__ = [
+    "tans_encode_interleaved",
+    "gpu_tans_decode",
+    "fp8_memcpy",
+    "fp8_vecadd_raw",
+    "fp8_vecadd_fused_tans",
+]
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _check_dev(name: str, t: torch.Tensor, dtype: torch.dtype) -> None:
+    _require(t.is_cuda, f"{name} must be CUDA")
+    _require(t.dtype == dtype, f"{name} must be {dtype}")
+    _require(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def _check_cpu(name: str, t: torch.Tensor, dtype: torch.dtype) -> None:
+    _require(t.device.type == "cpu", f"{name} must be a CPU tensor")
+    _require(t.dtype == dtype, f"{name} must be {dtype}")
+    _require(t.is_contiguous(), f"{name} must be contiguous")
+
+
+def log2_states(n: int) -> int:
+    """log2 of a table size, checking it is a supported alphabet's."""
+    _require(n in (1 << TANS_PAIR_LOG2L, 1 << TANS_NIBBLE_LOG2L),
+             f"table size must be 2^{TANS_PAIR_LOG2L} (pair) or 2^{TANS_NIBBLE_LOG2L} "
+             f"(nibble); got {n}")
+    return n.bit_length() - 1
+
+
+def tans_encode_interleaved(symbols: torch.Tensor, freqs: torch.Tensor,
+                            spread: torch.Tensor):
+    """CPU tANS encoder -> wave64 lane layout.  (csrc/tans_codec.cpp:69-196)
+
+    symbols [K, S] uint8 (one symbol per decode step), freqs int32 summing to
+    L = spread.numel(), spread [L] int32.  Returns (compressed uint8,
+    states uint16 [K], offsets int64 [ceil(K/64)+1], partial uint8 [0])."""
+    _require(symbols.dim() == 2, "symbols must be [K, N]")
+    _check_cpu("symbols", symbols, torch.uint8)
+    _check_cpu("freqs", freqs, torch.int32)
+    _check_cpu("spread", spread, torch.int32)
+    L = spread.numel()
+    _require(L > 0 and (L & (L - 1)) == 0 and L <= 4096, "spread size must be a power of two <= 4096")
+    K, S = symbols.shape
+    handle = ctypes.c_void_p()
+    comp_bytes = ctypes.c_int64()
+    n_off = ctypes.c_int64()
+    check(lib.tans_encode_begin(_ptr(symbols), K, S, _ptr(freqs), freqs.numel(), _ptr(spread),
+                                L.bit_length() - 1, ctypes.byref(handle),
+                                ctypes.byref(comp_bytes), ctypes.byref(n_off)),
+          "tans_encode_interleaved")
+    try:
+        comp = torch.empty(comp_bytes.value, dtype=torch.uint8)
+        states = torch.empty(K, dtype=torch.uint16)
+        offsets = torch.empty(n_off.value, dtype=torch.int64)
+    except BaseException:
+        lib.tans_encode_free(handle)
+        raise
+    check(lib.tans_encode_finish(handle, _ptr(comp), _ptr(states), _ptr(offsets)),
+          "tans_encode_interleaved")
+    return comp, states, offsets, torch.empty(0, dtype=torch.uint8)
+
+
+def _groups(K: int) -> int:
+    return (K + TANS_LANES - 1) // TANS_LANES
+
+
+def _sm_bytes(K: int, N: int) -> int:
+    return ((N + TANS_TILE - 1) // TANS_TILE) * K * 8
+
+
+def gpu_tans_decode(compressed: torch.Tensor, offsets: torch.Tensor, states: torch.Tensor,
+                    partial_cnts: torch.Tensor, sign_mantissa: torch.Tensor,
+                    spread: torch.Tensor, freqs: torch.Tensor,
+                    n_fp8_per_stream: int) -> torch.Tensor:
+    """Standalone decode -> uint8 [n_fp8_per_stream, K].  (csrc/tans_decode.cu:159-210)
+
+    The decode table is built on the device from spread/freqs, without the
+    reference's host round trip."""
+    _check_dev("compressed", compressed, torch.uint8)
+    _check_dev("offsets", offsets, torch.int64)
+    _check_dev("states", states, torch.uint16)
+    _check_dev("sign_mantissa", sign_mantissa, torch.uint8)
+    _check_dev("spread", spread, torch.int32)
+    _check_dev("freqs", freqs, torch.int32)
+    N = int(n_fp8_per_stream)
+    _require(N >= 0 and N % 2 == 0, "n_fp8_per_stream must be even")
+    K = states.numel()
+    _require(offsets.numel() == _groups(K) + 1, "offsets must have n_groups + 1 entries")
+    _require(sign_mantissa.numel() == _sm_bytes(K, N), "sign_mantissa has the wrong shape")
+    log2L = log2_states(spread.numel())
+    nsym = freqs.numel()
+    _require((nsym, log2L) in ((256, TANS_PAIR_LOG2L), (16, TANS_NIBBLE_LOG2L)),
+             "freqs must hold 256 pair or 16 nibble frequencies matching the spread size")
+    dev = compressed.device
+    out = torch.empty((N, K), dtype=torch.uint8, device=dev)
+    if K == 0 or N == 0:
+        return out
+    with torch.cuda.device(dev):
+        table = torch.empty(2 << log2L, dtype=torch.int32, device=dev)
+        stream = _stream(dev)
+        check(lib.tans_build_decode_table_device(_ptr(spread), _ptr(freqs), nsym, log2L,
+                                                 _ptr(table), stream), "gpu_tans_decode")
+        check(lib.tans_decode(_ptr(compressed), compressed.numel(), _ptr(offsets), _ptr(states),
+                              _ptr(sign_mantissa), _ptr(table), log2L, K, N, _ptr(out), stream),
+              "gpu_tans_decode")
+    return out
+
+
+def fp8_memcpy(A: torch.Tensor) -> torch.Tensor:
+    """C[i] = A[i] through 16-byte streaming loads.  (csrc/fp8_memcpy.cu:45-64)"""
+    _check_dev("A", A, torch.uint8)
+    _require(A.numel() % 16 == 0, "A length must be a multiple of 16")
+    C = torch.empty_like(A)
+    with torch.cuda.device(A.device):
+        check(lib.tans_fp8_memcpy(_ptr(A), _ptr(C), A.numel(), _stream(A.device)), "fp8_memcpy")
+    return C
+
+
+def fp8_vecadd_raw(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """C[i] = fp8(float(A[i]) + float(B[i])), RNE, saturating.  (csrc/vecadd.cu:268-288)"""
+    _check_dev("A", A, torch.uint8)
+    _check_dev("B", B, torch.uint8)
+    _require(A.numel() == B.numel(), "A and B must have the same length")
+    _require(A.numel() % 16 == 0, "A/B length must be a multiple of 16")
+    _require(A.device == B.device, "A and B must be on the same device")
+    C = torch.empty_like(A)
+    with torch.cuda.device(A.device):
+        check(lib.tans_fp8_vecadd_raw(_ptr(A), _ptr(B), _ptr(C), A.numel(), _stream(A.device)),
+              "fp8_vecadd_raw")
+    return C
+
+
+def fp8_vecadd_fused_tans(a_comp: torch.Tensor, a_offsets: torch.Tensor, a_states: torch.Tensor,
+                          a_partial: torch.Tensor, a_sm: torch.Tensor,
+                          b_comp: torch.Tensor, b_offsets: torch.Tensor, b_states: torch.Tensor,
+                          b_partial: torch.Tensor, b_sm: torch.Tensor,
+                          decode_tbl: torch.Tensor, n_fp8_per_stream: int) -> torch.Tensor:
+    """Fused tANS decode of A and B + FP8 add -> tiled uint8 [N/16 * K * 16].
+    (csrc/vecadd.cu:290-393)"""
+    for name, t in (("a_comp", a_comp), ("a_sm", a_sm), ("b_comp", b_comp), ("b_sm", b_sm)):
+        _check_dev(name, t, torch.uint8)
+    _check_dev("a_offsets", a_offsets, torch.int64)
+    _check_dev("b_offsets", b_offsets, torch.int64)
+    _check_dev("a_states", a_states, torch.uint16)
+    _check_dev("b_states", b_states, torch.uint16)
+    _check_dev("decode_tbl", decode_tbl, torch.int32)
+    N = int(n_fp8_per_stream)
+    _require(N >= 0 and N % 16 == 0, "n_fp8_per_stream must be divisible by 16")
+    K = a_states.numel()
+    _require(b_states.numel() == K, "A/B stream counts must match")
+    _require(a_offsets.numel() == _groups(K) + 1 and b_offsets.numel() == _groups(K) + 1,
+             "offset tensors must have n_groups + 1 entries")
+    _require(a_sm.numel() == _sm_bytes(K, N) and b_sm.numel() == _sm_bytes(K, N),
+             "sign/mantissa tensors have the wrong tiled size")
+    _require(decode_tbl.numel() % 2 == 0, "decode_tbl must hold 2 words per state")
+    log2L = log2_states(decode_tbl.numel() // 2)
+    dev = a_comp.device
+    for t in (a_offsets, a_states, a_sm, b_comp, b_offsets, b_states, b_sm, decode_tbl):
+        _require(t.device == dev, "all tensors must be on one device")
+    out = torch.empty(K * N, dtype=torch.uint8, device=dev)
+    if K == 0 or N == 0:
+        return out
+    with torch.cuda.device(dev):
+        check(lib.tans_fp8_vecadd_fused(_ptr(a_comp), a_comp.numel(), _ptr(a_offsets),
+                                        _ptr(a_states), _ptr(a_sm), _ptr(b_comp), b_comp.numel(),
+                                        _ptr(b_offsets), _ptr(b_states), _ptr(b_sm),
+                                        _ptr(decode_tbl), log2L, K, N, _ptr(out), _stream(dev)),
+              "fp8_vecadd_fused_tans")
+    return out

@@ -1,0 +1,170 @@
+"""tANS table construction and FP8 stream preparation (drop-in for the
+reference's rans_vectoradd/tans_codec.py).
+
+The exponent nibble e = (b >> 3) & 15 of each FP8 E4M3FN byte is tANS-coded;
+the sign and mantissa bits pass through as packed nibbles.  Two alphabets:
+
+* ``"pair"`` (default, as the reference): one symbol e0*16+e1 per two
+  elements, L = 2^12 states, pair probabilities = outer product of the
+  nibble marginals (reference tans_codec.py:123-130).
+* ``"nibble"``: one symbol per element, 16 symbols, L = 2^11 states.
+
+The encoded layout (wave64 lane groups, one shared word stream per group,
+16-element sign/mantissa tiles) is described in include/tans_amd.h.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _C
+from ._lib import TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PAIR_LOG2L, check, lib
+
+PAIR_L = 1 << TANS_PAIR_LOG2L
+NIBBLE_L = 1 << TANS_NIBBLE_LOG2L
+L = PAIR_L
+M = L
+BLOCK_STREAMS = TANS_LANES   # lanes per group (reference: 128 streams per block)
+TILE_PAIRS = 8               # sign/mantissa tile: 8 pairs = 16 elements
+
+ALPHABETS = {"pair": (256, PAIR_L, 2), "nibble": (16, NIBBLE_L, 1)}
+
+
+def sigma_for(n_states: int) -> int:
+    """Hash-walk stride (n/2 + n/8 + 3), odd for n >= 8 so the walk visits
+    every slot (reference tans_codec.py:26)."""
+    return (n_states >> 1) + (n_states >> 3) + 3
+
+
+SIGMA = sigma_for(L)
+
+
+def quantize_freqs(probs, target: int = M) -> np.ndarray:
+    """Scale probabilities to integer frequencies summing to ``target``.
+
+    Same rule as the reference (tans_codec.py:30-46): round to nearest, give
+    every p > 0 at least 1 and every p == 0 exactly 0, then move one unit at
+    a time to (or from) the symbol whose rounding error is largest, lowest
+    index first on ties.  The result is a drop-in for the reference's."""
+    p = np.asarray(probs, dtype=np.float64).reshape(-1)
+    scaled = p * target
+    f = np.where(p > 0, np.maximum(np.rint(scaled), 1.0), 0.0).astype(np.int64)
+    short = int(target - f.sum())
+    while short > 0:                       # under target: grow most under-served
+        gain = np.where(p > 0, scaled - f, -np.inf)
+        f[int(np.argmax(gain))] += 1
+        short -= 1
+    while short < 0:                       # over target: shrink most over-served
+        excess = np.where((p > 0) & (f <= 1), -np.inf, f - scaled)
+        f[int(np.argmax(excess))] -= 1
+        short += 1
+    if int(f.sum()) != target:
+        raise ValueError("quantize_freqs: probabilities cannot fill the target")
+    return f.astype(np.int32)
+
+
+def build_spread(freqs, n_states: int | None = None) -> np.ndarray:
+    """Slot -> symbol map: symbols in ascending order each take f_s slots
+    along the walk slot_k = k * SIGMA mod L (reference tans_codec.py:49-60).
+    ``n_states`` defaults to sum(freqs)."""
+    f = np.asarray(freqs, dtype=np.int64).reshape(-1)
+    n = int(f.sum()) if n_states is None else int(n_states)
+    if int(f.sum()) != n or n & (n - 1):
+        raise ValueError("build_spread: freqs must sum to a power of two")
+    step = sigma_for(n)
+    symbols = np.repeat(np.arange(f.size, dtype=np.int32), f)
+    slots = (np.arange(n, dtype=np.int64) * step) % n
+    spread = np.full(n, -1, dtype=np.int32)
+    spread[slots] = symbols
+    if (spread < 0).any():
+        raise ValueError("build_spread: walk does not cover every slot")
+    return spread
+
+
+def build_decode_table(spread, freqs) -> torch.Tensor:
+    """Decode table for the GPU kernels: int32 [2 * L], two words per state
+    (layout in include/tans_amd.h).  Alphabet from len(freqs): 256 -> pair
+    (L must be 4096), 16 -> nibble (L must be 2048)."""
+    sp = np.ascontiguousarray(np.asarray(spread, dtype=np.int32).reshape(-1))
+    fr = np.ascontiguousarray(np.asarray(freqs, dtype=np.int32).reshape(-1))
+    n = sp.size
+    out = torch.empty(2 * n, dtype=torch.int32)
+    check(lib.tans_build_decode_table(ctypes.c_void_p(sp.ctypes.data),
+                                      ctypes.c_void_p(fr.ctypes.data), fr.size,
+                                      max(n.bit_length() - 1, 0),
+                                      ctypes.c_void_p(out.data_ptr())),
+          "build_decode_table")
+    return out
+
+
+def split_fp8(fp8_bytes: torch.Tensor, alphabet: str = "pair"):
+    """FP8 bytes [K, N] -> (symbols [K, N/2] or [K, N] uint8, packed
+    sign/mantissa tiles uint8 [ceil(N/16), K, 8])."""
+    nsym, _, sps = ALPHABETS[alphabet]
+    x = fp8_bytes.contiguous()
+    K, N = x.shape
+    S = N // sps
+    symbols = torch.empty((K, S), dtype=torch.uint8)
+    sm = torch.empty(((N + 15) // 16, K, 8), dtype=torch.uint8)
+    check(lib.tans_split_fp8(ctypes.c_void_p(x.data_ptr()), K, N, sps,
+                             ctypes.c_void_p(symbols.data_ptr()), ctypes.c_void_p(sm.data_ptr())),
+          "split_fp8")
+    return symbols, sm
+
+
+def symbol_freqs(exp_freqs, alphabet: str = "pair") -> np.ndarray:
+    """Quantised symbol frequencies from a 16-entry exponent histogram."""
+    nsym, n_states, _ = ALPHABETS[alphabet]
+    # normalised in float32, as the reference does (tans_codec.py:126-128),
+    # so the quantised frequencies match its pair_freqs
+    p = np.asarray(exp_freqs, dtype=np.float32).reshape(-1)
+    if p.size != 16 or not p.sum() > 0 or (p < 0).any():
+        raise ValueError("exp_freqs must be 16 non-negative weights")
+    p = p / p.sum()
+    if nsym == 256:
+        p = (p[:, None] * p[None, :]).reshape(-1)
+    return quantize_freqs(p, target=n_states)
+
+
+def encode(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair"):
+    """tANS-encode FP8 bytes [K, N] (K lanes of N elements, N even).
+
+    Returns the reference's 7-tuple: (compressed uint8, states uint16 [K],
+    offsets int64 [ceil(K/64)+1], partial uint8 [0], sm uint8 tiles,
+    freqs int32, spread int32).  ``tile`` is accepted for the reference's
+    signature: 0 (standalone decode) and 8 (fused vecadd) give the same
+    16-element sign/mantissa tiles here; other values raise."""
+    if not (isinstance(fp8_bytes, torch.Tensor) and fp8_bytes.dim() == 2
+            and fp8_bytes.dtype == torch.uint8):
+        raise ValueError("fp8_bytes must be a 2-D uint8 tensor [K, N]")
+    if alphabet not in ALPHABETS:
+        raise ValueError(f"alphabet must be one of {sorted(ALPHABETS)}")
+    if tile not in (0, TILE_PAIRS):
+        raise ValueError(f"tile must be 0 or {TILE_PAIRS}")
+    K, N = fp8_bytes.shape
+    if N % 2:
+        raise ValueError("N must be even")
+    if isinstance(exp_freqs, torch.Tensor):
+        exp_freqs = exp_freqs.detach().cpu().float().numpy()
+    freqs = symbol_freqs(exp_freqs, alphabet)
+    spread = build_spread(freqs)
+    symbols, sm = split_fp8(fp8_bytes.cpu(), alphabet)
+    freqs_t = torch.from_numpy(freqs)
+    spread_t = torch.from_numpy(spread)
+    comp, states, offsets, partial = _C.tans_encode_interleaved(symbols, freqs_t, spread_t)
+    return comp, states, offsets, partial, sm, freqs_t, spread_t
+
+
+def untile(out_flat: torch.Tensor, K: int, N: int) -> torch.Tensor:
+    """Tiled fused-vecadd output [N/16, K, 16] -> row-major [K, N]
+    (the helper of the reference's test_vecadd_tans.py:20-27)."""
+    return out_flat.view(N // 16, K, 16).permute(1, 0, 2).reshape(K, N).contiguous()
+
+
+def compressed_bytes(comp, states, offsets, partial, sm) -> int:
+    """Bytes a decoder reads for one tensor, counted as the reference's bench
+    does (bench_vecadd.py:75-78): payload + sign/mantissa + metadata."""
+    return (comp.numel() + sm.numel() + states.numel() * 2 + offsets.numel()
+            * offsets.element_size() + partial.numel())
