@@ -12,19 +12,35 @@
 //                          (csrc/tans_decode.cu:125-155)
 //
 // Decoder design.  One wave64 decodes one 64-lane group; each lane owns one
-// tANS state.  The table lives in LDS as 8-byte entries indexed by a byte
-// offset kept in the state register, so one step is: ds_read_b64, bit-field
-// extract of nb bits from a 64-bit LSB-first bit buffer, a 64-bit shift, and
-// one shift-add for the next table offset.  Every second step the lane
-// refills 32 bits from its next word row when 32 or fewer bits remain (two
-// steps read at most 2*12 bits).  The next word is always loaded one refill
-// ahead.  FP8 bytes are rebuilt four at a time: the table carries each
-// exponent pre-shifted to bits 6:3 of a byte, a v_perm gathers four of them,
-// and one v_bfi merges the sign/mantissa word.
+// tANS state.  The decode table lives in LDS as 8-byte entries addressed by
+// a byte offset kept in the state register.  A lane's unread bits sit in a
+// 64-bit window (hi:lo) read from bit `pos`; one step is a ds_read_b64 of
+// the entry, a 64-bit shift of the window, a bit-field extract of nb bits,
+// one shift-add for the next entry's offset and pos += nb.
+//
+// Before every second step, each lane holding fewer than 24 unread bits
+// takes the next word of the group's stream: the ballot of those lanes, an
+// mbcnt for each lane's rank and one ds_read_b32 from the wave's LDS ring.
+// The ring holds kSlots segments of 128 words (one 8-byte load per lane)
+// plus a 64-word mirror of its first words, so a wave's 64 consecutive reads
+// never wrap.  Segments are fetched by an unconditional per-stage load
+// whose address (the next segment, or a cache-hot idle address when the ring
+// is full or the stream is done) is chosen by scalar code; the data is
+// written into the ring kDelay stages later.  A stage is two refill checks,
+// so at most 128 words are handed out per stage, and kSlots = kDelay + 2
+// guarantees every segment is in the ring before a lane asks for it.  All
+// vector-memory instructions run in a fixed order, so the compiler's
+// wait counts stay exact and no stage waits for a full memory round trip.
+//
+// FP8 bytes are rebuilt four at a time: the table carries each exponent
+// pre-shifted to bits 6:3 of a byte, a v_perm gathers four of them and one
+// v_bfi merges the sign/mantissa word.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <climits>
 #include <string>
+#include <type_traits>
 
 #include "../../include/tans_amd.h"
 
@@ -34,22 +50,31 @@ namespace {
 
 constexpr int kLanes = 64;
 constexpr int kTile = 16;
-constexpr int kBlock = 256;                 // 4 waves = 4 groups per workgroup
 constexpr uint32_t kExpMask = 0x78787878u;  // exponent field of 4 FP8 bytes
 
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 // ---------------------------------------------------------------------
-// FP8 E4M3FN add of 4 packed bytes.  The bytes go to f16 pairs (exact), are
-// added with v_pk_add_f16 (the f16 sum of two E4M3 values rounds only where
-// the E4M3 rounding cannot be affected: the dropped bits lie below a quarter
-// of an E4M3 ulp), clamped to +-448 with IEEE-754-2019 maximum/minimum so a
-// NaN stays NaN, and converted back with round-to-nearest-even.  The gfx950
-// conversions do not saturate (an out-of-range value becomes NaN), hence the
-// clamp.  Shared by the raw and fused kernels so both give the same bytes.
+// FP8 E4M3FN add of 4 packed bytes.  The bytes go to f16 pairs (exact) and
+// are added with v_pk_add_f16.  E4M3 has p = 4 significant bits and f16
+// p' = 11 >= 2p + 2, so rounding the exact sum first to f16 and then to E4M3
+// (both nearest-even) equals a single rounding of the exact sum.  The sum
+// is clamped to +-448 with IEEE-754-2019 maximum/minimum (a NaN stays NaN)
+// and converted back with round-to-nearest-even: the gfx950 conversions do
+// not saturate (an out-of-range value becomes 0x7E/0x7F), hence the clamp.
+// Shared by the raw and fused kernels so both give the same bytes.
 // ---------------------------------------------------------------------
-typedef float v2f __attribute__((ext_vector_type(2)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef short v2s __attribute__((ext_vector_type(2)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ v2h sat448(v2h v) {
     const v2h lo = {(_Float16)-448.0f, (_Float16)-448.0f};
@@ -62,7 +87,9 @@ __device__ __forceinline__ uint32_t add4_fp8(uint32_t a, uint32_t b) {
     const v2h a23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(a, 1.0f, true);
     const v2h b01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(b, 1.0f, false);
     const v2h b23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(b, 1.0f, true);
-    v2s r = {0, 0};
+    // the first conversion fills bytes 0-1, the second bytes 2-3; `a` only
+    // supplies the don't-care initial contents
+    v2s r = __builtin_bit_cast(v2s, a);
     r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(r, sat448(a01 + b01), 1.0f, false);
     r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(r, sat448(a23 + b23), 1.0f, true);
     return __builtin_bit_cast(uint32_t, r);
@@ -78,44 +105,26 @@ __device__ __forceinline__ v4u add16_fp8(v4u a, v4u b) {
 }
 
 // ---------------------------------------------------------------------
-// Streaming kernels: each thread moves kUnroll 16-byte vectors, strided by
-// the block so every load instruction of a wave covers 1 KiB.
+// Streaming kernels: one 16-byte vector per thread and tensor, non-temporal
+// loads and stores.  Measured on MI355X this shape moves more bytes per
+// second than grid-stride loops or several vectors per thread.
 // ---------------------------------------------------------------------
-constexpr int kUnroll = 4;
+constexpr int kBlock = 256;
 
 __global__ __launch_bounds__(kBlock) void fp8_copy_kernel(const v4u* __restrict__ a,
                                                           v4u* __restrict__ c, int64_t n_vec) {
-    const int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x;
-    v4u v[kUnroll];
-    #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + (int64_t)u * kBlock;
-        if (i < n_vec) v[u] = __builtin_nontemporal_load(a + i);
-    }
-    #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + (int64_t)u * kBlock;
-        if (i < n_vec) __builtin_nontemporal_store(v[u], c + i);
-    }
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i < n_vec) __builtin_nontemporal_store(__builtin_nontemporal_load(a + i), c + i);
 }
 
 __global__ __launch_bounds__(kBlock) void fp8_add_kernel(const v4u* __restrict__ a,
                                                          const v4u* __restrict__ b,
                                                          v4u* __restrict__ c, int64_t n_vec) {
-    const int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x;
-    v4u va[kUnroll], vb[kUnroll];
-    #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + (int64_t)u * kBlock;
-        if (i < n_vec) {
-            va[u] = __builtin_nontemporal_load(a + i);
-            vb[u] = __builtin_nontemporal_load(b + i);
-        }
-    }
-    #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
-        const int64_t i = base + (int64_t)u * kBlock;
-        if (i < n_vec) __builtin_nontemporal_store(add16_fp8(va[u], vb[u]), c + i);
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i < n_vec) {
+        const v4u va = __builtin_nontemporal_load(a + i);
+        const v4u vb = __builtin_nontemporal_load(b + i);
+        __builtin_nontemporal_store(add16_fp8(va, vb), c + i);
     }
 }
 
@@ -125,7 +134,7 @@ __global__ __launch_bounds__(kBlock) void fp8_add_kernel(const v4u* __restrict__
 // ---------------------------------------------------------------------
 __global__ __launch_bounds__(256) void table_kernel(const int32_t* __restrict__ spread,
                                                     const int32_t* __restrict__ freqs, int nsym,
-                                                    int log2L, uint2* __restrict__ table) {
+                                                    int log2L, v2u* __restrict__ table) {
     __shared__ int32_t sp[1 << TANS_PAIR_LOG2L];
     const uint32_t L = 1u << log2L;
     for (uint32_t i = threadIdx.x; i < L; i += blockDim.x) sp[i] = spread[i];
@@ -141,97 +150,178 @@ __global__ __launch_bounds__(256) void table_kernel(const int32_t* __restrict__ 
         const uint32_t xp = f + rank++;
         const int nb = xp ? log2L - (31 - __builtin_clz(xp)) : 0;
         const uint32_t base = xp << nb;
-        table[slot] = make_uint2((uint32_t)nb | ex, (base - L) * 8u);
+        table[slot] = v2u{(uint32_t)nb | ex, (base - L) * 8u};
     }
 }
 
 // ---------------------------------------------------------------------
-// Per-lane tANS decoder and the wave's staged word stream.
-//
-// A group's words are consumed strictly in stream order, so the wave stages
-// them through a 512-word LDS ring: segment s (stream words 256s..256s+255)
-// lives in ring half s&1 and is loaded with one 16-byte load per lane two
-// segments ahead of use.  At a refill check the lanes that need bits take
-// consecutive words: lane rank from mbcnt over the ballot, the wave position
-// advanced by its popcount.
+// Buffer resources.  Loads and stores in the decode loops go through raw
+// buffer descriptors: a wave-uniform base, a 32-bit lane offset, and a byte
+// bound past which loads return zero and stores are dropped (so idle fetch
+// slots, lanes past K and malformed offsets never touch memory outside the
+// tensors).  0x00020000 is the gfx9-family descriptor word 3 for raw
+// 32-bit-element access.
 // ---------------------------------------------------------------------
-constexpr int kRefillBelow = 24;   // refill a lane holding fewer bits than this
-constexpr int kSegWords = 256;     // 64 lanes x 16 bytes
-constexpr int kRingWords = 2 * kSegWords;
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kNT = 2;   // cache policy: non-temporal
 
-struct WaveStream {
-    const uint32_t* comp;   // whole compressed buffer
-    int64_t seg_base;       // word index of segment 0 of this group
-    int64_t max_start;      // last legal segment start (buffer words - 256)
-    uint32_t* ring;         // this wave's ring (LDS)
-    uint32_t pos;           // next unconsumed stream word
-    uint32_t boundary;      // pos at which the oldest ring segment is free
-    uint32_t next_seg;      // segment index held in `pend`
-    v4u pend;               // segment next_seg, in flight
+__device__ __forceinline__ Rsrc rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             kRsrcWord3);
+}
+
+// ---------------------------------------------------------------------
+// Decoder building blocks.
+// ---------------------------------------------------------------------
+constexpr int kRefillBelow = 24;           // a lane with fewer unread bits takes a word
+typedef v4u Seg;                           // one segment: 16 bytes per lane
+constexpr int kSegWords = 4 * kLanes;
+constexpr int kChecksPerStage = 4;         // a stage is 4 refill checks (8 steps)
+constexpr int kDelay = 1;                  // stages from a segment load to its ring write
+constexpr int kSlots = kDelay + 2;
+constexpr int kRingWords = kSlots * kSegWords;
+constexpr int kMirrorWords = kLanes;
+constexpr int kRingAlloc = kRingWords + kMirrorWords;
+constexpr int kDecWaves = 16;              // waves per workgroup
+constexpr int kSmAhead = 4;                // sign/mantissa rows are loaded this many tiles ahead
+constexpr int kDecBlock = kDecWaves * kLanes;
+// At most kChecksPerStage * 64 words are handed out per stage.  A segment is
+// fetched once the one kSlots earlier in its slot is consumed; it is written
+// kDelay stages later and first read no earlier than
+// (kSlots - 1) * kSegWords - kChecksPerStage * 64 words after the fetch
+// decision.
+static_assert((kSlots - 1) * kSegWords >= (kDelay + 1) * kChecksPerStage * kLanes,
+              "ring too small for the delay");
+
+// Wave-uniform state of one group's word stream.
+struct Feed {
+    const char* next;       // next segment to fetch
+    uint32_t len;           // words in the group's stream (clamped to the buffer)
+    int32_t room;           // bytes from `next` to the end of the buffer (may go below 0)
+    uint32_t next_word;     // stream word index of `next`
+    uint32_t next_slot;     // ring slot of `next`
+    uint32_t handed;        // words handed to lanes so far
+    uint32_t ring_b;        // byte offset in the ring of word `handed`
+    int32_t dest[kDelay];   // ring slot of the fetch issued at each stage, -1 if idle
+    uint32_t* ring;         // this wave's ring for this stream (LDS)
 };
 
-__device__ __forceinline__ v4u load_segment(const WaveStream& s, uint32_t seg, int lane) {
-    int64_t start = s.seg_base + (int64_t)seg * kSegWords;
-    start = start < 0 ? 0 : (start > s.max_start ? s.max_start : start);
-    return __builtin_nontemporal_load(reinterpret_cast<const v4u*>(s.comp + start) + lane);
-}
-
-__device__ __forceinline__ void store_segment(WaveStream& s, uint32_t seg, v4u v, int lane) {
-    reinterpret_cast<v4u*>(s.ring + (seg & 1u) * kSegWords)[lane] = v;
-}
-
-__device__ __forceinline__ void stream_init(WaveStream& s, const uint32_t* comp, int64_t comp_words,
-                                            int64_t start, uint32_t* ring, int lane) {
-    s.comp = comp;
-    s.seg_base = start;
-    s.max_start = comp_words - kSegWords;
-    s.ring = ring;
-    s.pos = 0;
-    s.boundary = kSegWords;
-    const v4u s0 = load_segment(s, 0, lane);
-    const v4u s1 = load_segment(s, 1, lane);
-    store_segment(s, 0, s0, lane);
-    store_segment(s, 1, s1, lane);
-    s.next_seg = 2;
-    s.pend = load_segment(s, 2, lane);
-}
-
-struct LaneDec {
-    uint64_t buf;   // unread bits, LSB first
-    uint32_t cnt;   // bits 7:0 = valid bits in buf (upper bits: junk)
-    uint32_t x8;    // (state - L) * 8: byte offset of the table entry
+// Per-lane decoder state.
+struct Lane {
+    uint32_t lo, hi;   // 64-bit window of stream bits, bit `pos` is the next unread one
+    int32_t pos;       // active lanes: [0, 64]; idle lanes: far below 0, never refill
+    uint32_t x8;       // (state - L) * 8: byte offset of the state's table entry
 };
 
-// Refill check: lanes with fewer than 24 bits take the next stream words.
-__device__ __forceinline__ void refill(LaneDec& d, WaveStream& s, bool active, int lane) {
-    const bool need = active && (d.cnt & 0xFFu) < (uint32_t)kRefillBelow;
+// Segment `next` (the part of it inside the buffer), or nothing.  The bound
+// is the room left in the buffer; a single max keeps it a scalar value (a
+// clamp would become a vector med3, and a non-uniform descriptor makes the
+// compiler loop over its values).
+__device__ __forceinline__ Seg fetch_seg(const Feed& f, bool fetch, int lane) {
+    const int32_t room = f.room > 0 ? f.room : 0;
+    return __builtin_amdgcn_raw_buffer_load_b128(rsrc(f.next, fetch ? (uint32_t)room : 0u),
+                                                 (uint32_t)lane * 16u, 0, 0);
+}
+
+__device__ __forceinline__ void write_seg(uint32_t* ring, int32_t slot, Seg v, int lane) {
+    reinterpret_cast<Seg*>(ring + slot * kSegWords)[lane] = v;
+    if (slot == 0 && lane < kMirrorWords / 4)
+        reinterpret_cast<Seg*>(ring + kRingWords)[lane] = v;
+}
+
+__device__ __forceinline__ void feed_advance(Feed& f) {
+    f.next += kSegWords * 4;
+    f.room -= kSegWords * 4;
+    f.next_word += kSegWords;
+    f.next_slot = f.next_slot == (uint32_t)(kSlots - 1) ? 0u : f.next_slot + 1;
+}
+
+// Clamp group g's stream to the buffer, fetch and write its first kSlots
+// segments.
+__device__ __forceinline__ void feed_init(Feed& f, const uint32_t* comp, int64_t words,
+                                          const int64_t* off, int64_t g, uint32_t* ring, int lane,
+                                          Seg (&pend)[kDelay]) {
+    int64_t s = off[g], e = off[g + 1];
+    s = s < 0 ? 0 : (s > words ? words : s);
+    e = e < s ? s : (e > words ? words : e);
+    const int64_t room = (words - s) * 4;
+    f.next = reinterpret_cast<const char*>(comp + s);
+    f.len = (uint32_t)(e - s);
+    f.room = room > 0x7FFFFFFF ? 0x7FFFFFFF : (int32_t)room;
+    f.next_word = 0;
+    f.next_slot = 0;
+    f.handed = 0;
+    f.ring_b = 0;
+    f.ring = ring;
+    Seg first[kSlots];
+    #pragma unroll
+    for (int i = 0; i < kSlots; i++) {
+        first[i] = fetch_seg(f, f.next_word < f.len, lane);
+        feed_advance(f);
+    }
+    #pragma unroll
+    for (int i = 0; i < kSlots; i++) write_seg(ring, i, first[i], lane);
+    #pragma unroll
+    for (int i = 0; i < kDelay; i++) {
+        f.dest[i] = -1;
+        pend[i] = Seg{0u, 0u, 0u, 0u};
+    }
+}
+
+// Start of stage ST: write the fetch issued kDelay stages ago, then issue
+// this stage's fetch.  The next segment is fetched when it exists and its
+// slot is free (the segment kSlots earlier is consumed); otherwise the load
+// has an empty bound and reads nothing.
+template <int ST>
+__device__ __forceinline__ void feed_stage(Feed& f, Seg (&pend)[kDelay], int lane) {
+    const int32_t d = f.dest[ST];
+    if (d >= 0) write_seg(f.ring, d, pend[ST], lane);
+    const uint32_t free_to = f.handed + (uint32_t)((kSlots - 1) * kSegWords) + 1;
+    const uint32_t lim = f.len < free_to ? f.len : free_to;
+    const bool fetch = f.next_word < lim;
+    pend[ST] = fetch_seg(f, fetch, lane);
+    f.dest[ST] = fetch ? (int32_t)f.next_slot : -1;
+    if (fetch) feed_advance(f);
+}
+
+// Refill check: lanes with fewer than 24 unread bits take the next words of
+// the stream, in lane order.  Every lane reads the ring (in bounds: the
+// mirror covers the 64 words past the ring end); only those that need a
+// word keep it, so there is no divergent branch.
+__device__ __forceinline__ void refill(Lane& l, Feed& f) {
+    const bool need = l.pos > 64 - kRefillBelow;
     const uint64_t m = __ballot(need);
-    if (m == 0) return;
-    if (need) {
-        const uint32_t idx = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)m, s.pos));
-        const uint32_t w = s.ring[idx & (kRingWords - 1)];
-        d.buf |= (uint64_t)w << (d.cnt & 63u);
-        d.cnt += 32u;
-    }
-    s.pos += (uint32_t)__popcll(m);
-    if (s.pos >= s.boundary) {
-        // the oldest segment is consumed: its half takes the pending one
-        store_segment(s, s.next_seg, s.pend, lane);
-        s.next_seg += 1;
-        s.pend = load_segment(s, s.next_seg, lane);
-        s.boundary += kSegWords;
-    }
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(
+        reinterpret_cast<const char*>(f.ring) + f.ring_b + rank * 4u);
+    l.lo = need ? l.hi : l.lo;
+    l.hi = need ? w : l.hi;
+    l.pos = need ? l.pos - 32 : l.pos;
+    const uint32_t c = (uint32_t)__popcll(m);
+    f.handed += c;
+    const uint32_t nb = f.ring_b + c * 4u;
+    const uint32_t wrapped = nb - (uint32_t)(kRingWords * 4);
+    f.ring_b = nb < wrapped ? nb : wrapped;   // (nb mod ring size), as an unsigned min
 }
 
-// One tANS step.  Returns the table's word0 (nb and the exponent bytes).
-__device__ __forceinline__ uint32_t dec_step(LaneDec& d, const uint2* __restrict__ tbl) {
-    const uint2 e = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(tbl) + d.x8);
-    const uint32_t bits = __builtin_amdgcn_ubfe((uint32_t)d.buf, 0u, e.x);  // width = e.x[4:0]
-    d.buf >>= (e.x & 63u);
-    d.x8 = (bits << 3) + e.y;
-    d.cnt -= e.x;   // bits 7:0 drop by nb; exponent bytes only touch bits 8+
+// One tANS step.  Returns the entry's word0: nb in bits 4:0, exponents in
+// bits 14:11 (and 22:19 for a pair symbol).
+__device__ __forceinline__ uint32_t dec_step(Lane& l, const v2u* __restrict__ tbl) {
+    const v2u e = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
+    const uint64_t win = ((uint64_t)l.hi << 32) | l.lo;
+    const uint32_t t = (uint32_t)(win >> (l.pos & 63));
+    const uint32_t bits = __builtin_amdgcn_ubfe(t, 0u, e.x);   // width = e.x[4:0]
+    l.x8 = (bits << 3) + e.y;
+    l.pos += (int32_t)(e.x & 0xFFu);
     return e.x;
+}
+
+__device__ __forceinline__ void lane_init(Lane& l, bool active, uint16_t state, uint32_t L) {
+    l.lo = l.hi = 0;
+    l.pos = active ? 64 : -(1 << 30);
+    l.x8 = ((uint32_t)(state - L) & (L - 1)) * 8u;
 }
 
 // Exponent fields of four consecutive elements, from two pair steps or four
@@ -256,179 +346,354 @@ __device__ __forceinline__ void compose8(uint32_t ex_lo, uint32_t ex_hi, uint32_
     out_hi = bfi(kExpMask, ex_hi, __builtin_amdgcn_alignbit(smw, smw, 4u));
 }
 
-// Decode one 16-element tile of two streams, their steps interleaved.
-template <int SPS>
-__device__ __forceinline__ void dec_tile2(LaneDec& da, WaveStream& sa, LaneDec& db, WaveStream& sb,
-                                          const uint2* __restrict__ tbl, bool active, int lane,
-                                          uint32_t ea[4], uint32_t eb[4]) {
-    if constexpr (SPS == 2) {
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            refill(da, sa, active, lane);
-            refill(db, sb, active, lane);
-            const uint32_t a0 = dec_step(da, tbl);
-            const uint32_t b0 = dec_step(db, tbl);
-            const uint32_t a1 = dec_step(da, tbl);
-            const uint32_t b1 = dec_step(db, tbl);
-            ea[q] = exp4_pair(a0, a1);
-            eb[q] = exp4_pair(b0, b1);
-        }
-    } else {
-        #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            uint32_t a[4], b[4];
-            #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                refill(da, sa, active, lane);
-                refill(db, sb, active, lane);
-                a[2 * h] = dec_step(da, tbl);
-                b[2 * h] = dec_step(db, tbl);
-                a[2 * h + 1] = dec_step(da, tbl);
-                b[2 * h + 1] = dec_step(db, tbl);
-            }
-            ea[q] = exp4_nib(a[0], a[1], a[2], a[3]);
-            eb[q] = exp4_nib(b[0], b[1], b[2], b[3]);
-        }
-    }
-}
-
-// Decode `n` elements (n <= 16, n even) of one stream into exponent words.
-template <int SPS>
-__device__ __forceinline__ void dec_tile1(LaneDec& d, WaveStream& s, const uint2* __restrict__ tbl,
-                                          bool active, int lane, int n, uint32_t ex[4]) {
-    if (n == kTile) {
-        if constexpr (SPS == 2) {
-            #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                refill(d, s, active, lane);
-                const uint32_t e0 = dec_step(d, tbl);
-                const uint32_t e1 = dec_step(d, tbl);
-                ex[q] = exp4_pair(e0, e1);
-            }
-        } else {
-            #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                refill(d, s, active, lane);
-                const uint32_t e0 = dec_step(d, tbl);
-                const uint32_t e1 = dec_step(d, tbl);
-                refill(d, s, active, lane);
-                const uint32_t e2 = dec_step(d, tbl);
-                const uint32_t e3 = dec_step(d, tbl);
-                ex[q] = exp4_nib(e0, e1, e2, e3);
-            }
-        }
-        return;
-    }
-    // ragged last tile
-    ex[0] = ex[1] = ex[2] = ex[3] = 0;
-    const int steps = n / SPS;
-    for (int q = 0; q < steps; q++) {
-        if ((q & 1) == 0) refill(d, s, active, lane);
-        const uint32_t e = dec_step(d, tbl);
-        if constexpr (SPS == 2) ex[q >> 1] |= ((e >> 8) & 0xFFFFu) << (16 * (q & 1));
-        else ex[q >> 2] |= ((e >> 8) & 0xFFu) << (8 * (q & 3));
-    }
-}
-
+// Copy the decode table into LDS.  Entries that would step outside the
+// table (nb > log2L or base + 2^nb > 2L) are replaced by a harmless one, so
+// a malformed table gives wrong bytes, never an out-of-range LDS access.
 template <uint32_t L>
-__device__ __forceinline__ void load_table(uint2* lds, const uint2* __restrict__ table) {
-    for (uint32_t i = threadIdx.x; i < L; i += blockDim.x) lds[i] = table[i];
+__device__ __forceinline__ void load_table(v2u* lds, const v2u* __restrict__ table) {
+    constexpr uint32_t log2L = 31 - __builtin_clz(L);
+    for (uint32_t i = threadIdx.x; i < L; i += blockDim.x) {
+        v2u e = table[i];
+        const uint32_t nb = e.x & 0xFFu;
+        const uint32_t base = e.y >> 3;
+        if (nb > log2L || (e.y & 7u) || base + (1u << nb) > L) e = v2u{e.x & ~0xFFu, 0u};
+        lds[i] = e;
+    }
 }
 
-constexpr int kWaves = 8;                  // waves (= groups) per workgroup
-constexpr int kDecBlock = kWaves * kLanes;
-
 template <int SPS>
+struct Alpha {
+    static constexpr uint32_t L = SPS == 2 ? (1u << TANS_PAIR_LOG2L) : (1u << TANS_NIBBLE_LOG2L);
+    static constexpr int kStagesPerTile = SPS == 2 ? 1 : 2;   // a stage is 8 steps
+};
+
+// LDS of a decoder workgroup.  The table comes first so that its entries'
+// byte offsets are their LDS addresses.
+template <int SPS, int C>
+struct DecSmem {
+    v2u tbl[Alpha<SPS>::L];
+    uint32_t rings[kDecWaves][C][kRingAlloc];
+    uint32_t progress;   // tiles finished by all waves of the workgroup
+};
+
+// Keep the waves of a workgroup abreast.  The SIMD arbiter prefers older
+// waves, so without this the first wave on a SIMD finishes its groups in
+// about half the time of the last, which then runs alone at a fraction of
+// the SIMD's throughput.  After each tile a wave adds one to the
+// workgroup's progress count and sets its priority from where it stands: a
+// wave more than a tile ahead of the average yields (it still issues when
+// the others stall), a wave behind the average goes first.
+__device__ __forceinline__ void pace(uint32_t* progress, int lane, uint32_t done, uint32_t live) {
+    uint32_t before = 0;
+    if (lane == 0) before = __hip_atomic_fetch_add(progress, 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+    before = __builtin_amdgcn_readfirstlane(before);
+    const uint32_t mine = done * live;   // compare done with before / live
+    if (mine > before + 2 * live) {
+        __builtin_amdgcn_s_setprio(0);
+    } else if (mine + live <= before) {
+        __builtin_amdgcn_s_setprio(3);
+    } else {
+        __builtin_amdgcn_s_setprio(1);
+    }
+}
+
+// C independent chains (a chain = one group's stream) decoded in lockstep
+// by one wave, so each lane interleaves C serial tANS states.
+template <int C>
+struct Chains {
+    Feed f[C];
+    Lane l[C];
+    Seg p[C][kDelay];
+};
+
+// Decode the 16 elements of one tile of every chain into exponent words
+// ex[c][4] (4 elements each).  ST0 is the pipeline stage of the tile's first
+// stage.
+template <int SPS, int ST0, int C>
+__device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ tbl, int lane,
+                                         uint32_t (&ex)[C][4]) {
+    static_for<0, Alpha<SPS>::kStagesPerTile>([&](auto H) {
+        constexpr int h = decltype(H)::value;
+        #pragma unroll
+        for (int c = 0; c < C; c++) feed_stage<(ST0 + h) % kDelay>(ch.f[c], ch.p[c], lane);
+        uint32_t e[C][8];
+        #pragma unroll
+        for (int q = 0; q < kChecksPerStage; q++) {
+            #pragma unroll
+            for (int c = 0; c < C; c++) refill(ch.l[c], ch.f[c]);
+            #pragma unroll
+            for (int c = 0; c < C; c++) e[c][2 * q] = dec_step(ch.l[c], tbl);
+            #pragma unroll
+            for (int c = 0; c < C; c++) e[c][2 * q + 1] = dec_step(ch.l[c], tbl);
+        }
+        #pragma unroll
+        for (int c = 0; c < C; c++) {
+            if constexpr (SPS == 2) {
+                #pragma unroll
+                for (int i = 0; i < 4; i++) ex[c][i] = exp4_pair(e[c][2 * i], e[c][2 * i + 1]);
+            } else {
+                ex[c][2 * h] = exp4_nib(e[c][0], e[c][1], e[c][2], e[c][3]);
+                ex[c][2 * h + 1] = exp4_nib(e[c][4], e[c][5], e[c][6], e[c][7]);
+            }
+        }
+    });
+}
+
+// ---------------------------------------------------------------------
+// Fused decode + add.  A wave decodes G groups of A and the same G groups
+// of B (C = 2G chains) and writes their sums, tiled [N/16, K, 16].
+// ---------------------------------------------------------------------
+template <int SPS, int G>
+struct FusedWave {
+    static constexpr int C = 2 * G;   // chain 2g: A of group g, 2g + 1: B of group g
+    Chains<C> ch;
+    v2u sm[C][kSmAhead];    // sign/mantissa words of tiles t .. t + kSmAhead - 1 (by t mod kSmAhead)
+    const char* pf[C];      // sign/mantissa row of the next prefetch (wave-uniform)
+    char* out_cur[G];       // output row of the current tile (wave-uniform)
+    uint32_t sm_bytes[G];   // bytes of a group's sm row (8 per lane in range)
+    const v2u* tbl;
+    uint32_t* progress;     // workgroup progress count (LDS)
+    uint32_t live;          // waves of the workgroup with groups to decode
+    int64_t sm_stride;      // bytes between tiles: K * 8
+    int64_t out_stride;     // K * 16
+    int n_tiles;
+    int lane;
+
+    // Tile t, with P = t mod kSmAhead.
+    template <int P>
+    __device__ __forceinline__ void tile(int t) {
+        uint32_t ex[C][4];
+        dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, C>(ch, tbl, lane, ex);
+        pace(progress, lane, (uint32_t)t, live);
+        #pragma unroll
+        for (int g = 0; g < G; g++) {
+            uint32_t wa[4], wb[4];
+            compose8(ex[2 * g][0], ex[2 * g][1], sm[2 * g][P].x, wa[0], wa[1]);
+            compose8(ex[2 * g][2], ex[2 * g][3], sm[2 * g][P].y, wa[2], wa[3]);
+            compose8(ex[2 * g + 1][0], ex[2 * g + 1][1], sm[2 * g + 1][P].x, wb[0], wb[1]);
+            compose8(ex[2 * g + 1][2], ex[2 * g + 1][3], sm[2 * g + 1][P].y, wb[2], wb[3]);
+            const v4u va = {wa[0], wa[1], wa[2], wa[3]};
+            const v4u vb = {wb[0], wb[1], wb[2], wb[3]};
+            __builtin_amdgcn_raw_buffer_store_b128(add16_fp8(va, vb),
+                                                   rsrc(out_cur[g], sm_bytes[g] * 2u),
+                                                   (uint32_t)lane * 16u, 0, kNT);
+            out_cur[g] += out_stride;
+        }
+        // sign/mantissa of tile min(t + kSmAhead, n_tiles - 1): the loads are unconditional
+        #pragma unroll
+        for (int c = 0; c < C; c++)
+            sm[c][P] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(pf[c], sm_bytes[c / 2]),
+                                                            (uint32_t)lane * 8u, 0, kNT);
+        if (t + kSmAhead + 1 < n_tiles) {
+            #pragma unroll
+            for (int c = 0; c < C; c++) pf[c] += sm_stride;
+        }
+    }
+};
+
+template <int SPS, int G>
 __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     const uint32_t* __restrict__ a_comp, int64_t a_words, const int64_t* __restrict__ a_off,
-    const uint16_t* __restrict__ a_st, const uint2* __restrict__ a_sm,
+    const uint16_t* __restrict__ a_st, const v2u* __restrict__ a_sm,
     const uint32_t* __restrict__ b_comp, int64_t b_words, const int64_t* __restrict__ b_off,
-    const uint16_t* __restrict__ b_st, const uint2* __restrict__ b_sm,
-    const uint2* __restrict__ table, int64_t K, int64_t n_tiles, v4u* __restrict__ out) {
-    constexpr uint32_t L = SPS == 2 ? (1u << TANS_PAIR_LOG2L) : (1u << TANS_NIBBLE_LOG2L);
-    __shared__ uint2 tbl[L];
-    __shared__ uint32_t rings[kWaves][2][kRingWords];
+    const uint16_t* __restrict__ b_st, const v2u* __restrict__ b_sm,
+    const v2u* __restrict__ table, int64_t K, int n_tiles, v4u* __restrict__ out) {
+    constexpr uint32_t L = Alpha<SPS>::L;
+    constexpr int C = 2 * G;
+    __shared__ DecSmem<SPS, C> smem;
+    v2u* tbl = smem.tbl;
     load_table<L>(tbl, table);
+    if (threadIdx.x == 0) smem.progress = 0;
+    __syncthreads();
     const int lane = threadIdx.x & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
-    const int64_t g = (int64_t)blockIdx.x * kWaves + wave;
-    const int64_t k = g * kLanes + lane;
-    const bool live = g * kLanes < K;   // wave-uniform
-    WaveStream sa, sb;
-    if (live) {
-        stream_init(sa, a_comp, a_words, a_off[g], rings[wave][0], lane);
-        stream_init(sb, b_comp, b_words, b_off[g], rings[wave][1], lane);
-    }
-    __syncthreads();   // table and first ring segments visible
-    if (!live) return;
-    const bool active = k < K;
-    LaneDec da, db;
-    da.buf = db.buf = 0;
-    da.cnt = db.cnt = 0;
-    da.x8 = ((active ? a_st[k] : L) - L) * 8u;
-    db.x8 = ((active ? b_st[k] : L) - L) * 8u;
-    uint2 sma = active ? a_sm[k] : make_uint2(0, 0);
-    uint2 smb = active ? b_sm[k] : make_uint2(0, 0);
-    for (int64_t t = 0; t < n_tiles; t++) {
-        uint2 na = make_uint2(0, 0), nb = make_uint2(0, 0);
-        if (active && t + 1 < n_tiles) {
-            na = a_sm[(t + 1) * K + k];
-            nb = b_sm[(t + 1) * K + k];
+    const int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
+    if (g0 * kLanes >= K) return;   // wave-uniform
+    const int64_t n_groups = (K + kLanes - 1) / kLanes;
+    const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * G;
+    FusedWave<SPS, G> w;
+    w.progress = &smem.progress;
+    w.live = (uint32_t)(wg_groups >= (int64_t)kDecWaves * G ? kDecWaves : (wg_groups + G - 1) / G);
+    w.lane = lane;
+    w.n_tiles = n_tiles;
+    w.tbl = tbl;
+    w.sm_stride = K * 8;
+    w.out_stride = K * 16;
+    #pragma unroll
+    for (int j = 0; j < G; j++) {
+        // a wave past the last group repeats it with no lanes in range
+        const int64_t g = g0 + j < n_groups ? g0 + j : n_groups - 1;
+        const int64_t k0 = g * kLanes;
+        const int lanes = g0 + j < n_groups ? (K - k0 < kLanes ? (int)(K - k0) : kLanes) : 0;
+        const bool active = lane < lanes;
+        const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
+        w.sm_bytes[j] = (uint32_t)lanes * 8u;
+        w.out_cur[j] = reinterpret_cast<char*>(out + k0);
+        feed_init(w.ch.f[2 * j], a_comp, a_words, a_off, g, smem.rings[wave][2 * j], lane,
+                  w.ch.p[2 * j]);
+        feed_init(w.ch.f[2 * j + 1], b_comp, b_words, b_off, g, smem.rings[wave][2 * j + 1], lane,
+                  w.ch.p[2 * j + 1]);
+        lane_init(w.ch.l[2 * j], active, a_st[k0 + lane_ld], L);
+        lane_init(w.ch.l[2 * j + 1], active, b_st[k0 + lane_ld], L);
+        const char* rows[2] = {reinterpret_cast<const char*>(a_sm + k0),
+                               reinterpret_cast<const char*>(b_sm + k0)};
+        #pragma unroll
+        for (int s = 0; s < 2; s++) {
+            const int c = 2 * j + s;
+            #pragma unroll
+            for (int i = 0; i < kSmAhead; i++) {
+                const int64_t ti = i < n_tiles ? i : n_tiles - 1;
+                w.sm[c][i] = __builtin_amdgcn_raw_buffer_load_b64(
+                    rsrc(rows[s] + ti * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+            }
+            const int64_t tn = kSmAhead < n_tiles ? kSmAhead : n_tiles - 1;
+            w.pf[c] = rows[s] + tn * w.sm_stride;
         }
-        uint32_t ea[4], eb[4];
-        dec_tile2<SPS>(da, sa, db, sb, tbl, active, lane, ea, eb);
-        uint32_t wa[4], wb[4];
-        compose8(ea[0], ea[1], sma.x, wa[0], wa[1]);
-        compose8(ea[2], ea[3], sma.y, wa[2], wa[3]);
-        compose8(eb[0], eb[1], smb.x, wb[0], wb[1]);
-        compose8(eb[2], eb[3], smb.y, wb[2], wb[3]);
-        const v4u va = {wa[0], wa[1], wa[2], wa[3]};
-        const v4u vb = {wb[0], wb[1], wb[2], wb[3]};
-        if (active) __builtin_nontemporal_store(add16_fp8(va, vb), out + t * K + k);
-        sma = na;
-        smb = nb;
     }
+    int t = 0;
+    for (; t + kSmAhead <= n_tiles; t += kSmAhead) {
+        w.template tile<0>(t);
+        w.template tile<1>(t + 1);
+        w.template tile<2>(t + 2);
+        w.template tile<3>(t + 3);
+    }
+    static_assert(kSmAhead == 4, "the loop above is unrolled for kSmAhead == 4");
+    if (t < n_tiles) w.template tile<0>(t);
+    if (t + 1 < n_tiles) w.template tile<1>(t + 1);
+    if (t + 2 < n_tiles) w.template tile<2>(t + 2);
 }
 
-template <int SPS>
-__global__ __launch_bounds__(kDecBlock) void decode_kernel(
-    const uint32_t* __restrict__ comp, int64_t words, const int64_t* __restrict__ off,
-    const uint16_t* __restrict__ st, const uint2* __restrict__ sm,
-    const uint2* __restrict__ table, int64_t K, int64_t N, uint8_t* __restrict__ out) {
-    constexpr uint32_t L = SPS == 2 ? (1u << TANS_PAIR_LOG2L) : (1u << TANS_NIBBLE_LOG2L);
-    __shared__ uint2 tbl[L];
-    __shared__ uint32_t rings[kWaves][kRingWords];
-    load_table<L>(tbl, table);
-    const int lane = threadIdx.x & (kLanes - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
-    const int64_t g = (int64_t)blockIdx.x * kWaves + wave;
-    const int64_t k = g * kLanes + lane;
-    const bool live = g * kLanes < K;
-    WaveStream s;
-    if (live) stream_init(s, comp, words, off[g], rings[wave], lane);
-    __syncthreads();
-    if (!live) return;
-    const bool active = k < K;
-    LaneDec d;
-    d.buf = 0;
-    d.cnt = 0;
-    d.x8 = ((active ? st[k] : L) - L) * 8u;
-    const int64_t n_tiles = (N + kTile - 1) / kTile;
-    for (int64_t t = 0; t < n_tiles; t++) {
-        const int64_t e0 = t * kTile;
+// ---------------------------------------------------------------------
+// Standalone decode: G groups of one tensor per wave; output [N, K]
+// (element-major), one byte per lane and element.
+// ---------------------------------------------------------------------
+template <int SPS, int G>
+struct DecodeWave {
+    Chains<G> ch;
+    v2u sm[G][2];
+    const char* pf[G];
+    uint32_t sm_bytes[G];
+    uint8_t* out[G];        // column k0 of row 0
+    bool active[G];
+    const v2u* tbl;
+    uint32_t* progress;
+    uint32_t live;
+    int64_t K, N, sm_stride;
+    int n_tiles;
+    int lane;
+
+    template <int P>
+    __device__ __forceinline__ void tile(int t) {
+        const int64_t e0 = (int64_t)t * kTile;
         const int n = (int)(N - e0 < kTile ? N - e0 : kTile);
-        const uint2 smw = active ? sm[t * K + k] : make_uint2(0, 0);
-        uint32_t ex[4], w[4];
-        dec_tile1<SPS>(d, s, tbl, active, lane, n, ex);
-        compose8(ex[0], ex[1], smw.x, w[0], w[1]);
-        compose8(ex[2], ex[3], smw.y, w[2], w[3]);
-        if (active) {
-            #pragma unroll
-            for (int i = 0; i < kTile; i++) {
-                if (i < n) out[(e0 + i) * K + k] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+        uint32_t ex[G][4];
+        if (n == kTile) {
+            dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, G>(ch, tbl, lane, ex);
+        } else {
+            dec_ragged<P>(n, ex);
+        }
+        pace(progress, lane, (uint32_t)t, live);
+        #pragma unroll
+        for (int g = 0; g < G; g++) {
+            uint32_t w[4];
+            compose8(ex[g][0], ex[g][1], sm[g][P].x, w[0], w[1]);
+            compose8(ex[g][2], ex[g][3], sm[g][P].y, w[2], w[3]);
+            if (active[g]) {
+                uint8_t* o = out[g] + e0 * K + lane;
+                #pragma unroll
+                for (int i = 0; i < kTile; i++)
+                    if (i < n) o[i * K] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
             }
         }
+        #pragma unroll
+        for (int g = 0; g < G; g++)
+            sm[g][P] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(pf[g], sm_bytes[g]),
+                                                            (uint32_t)lane * 8u, 0, kNT);
+        if (t + 3 < n_tiles) {
+            #pragma unroll
+            for (int g = 0; g < G; g++) pf[g] += sm_stride;
+        }
     }
+
+    // Last tile with fewer than 16 elements: the same stages, fewer steps.
+    template <int P>
+    __device__ __forceinline__ void dec_ragged(int n, uint32_t (&ex)[G][4]) {
+        constexpr int ST0 = (P * Alpha<SPS>::kStagesPerTile) % kDelay;
+        const int steps = n / SPS;
+        #pragma unroll
+        for (int g = 0; g < G; g++) ex[g][0] = ex[g][1] = ex[g][2] = ex[g][3] = 0;
+        static_for<0, Alpha<SPS>::kStagesPerTile>([&](auto H) {
+            constexpr int h = decltype(H)::value;
+            #pragma unroll
+            for (int g = 0; g < G; g++) feed_stage<(ST0 + h) % kDelay>(ch.f[g], ch.p[g], lane);
+            for (int q = 0; q < 2 * kChecksPerStage; q++) {
+                const int i = h * 2 * kChecksPerStage + q;
+                if (i >= steps) break;
+                #pragma unroll
+                for (int g = 0; g < G; g++) {
+                    if ((q & 1) == 0) refill(ch.l[g], ch.f[g]);
+                    const uint32_t e = dec_step(ch.l[g], tbl);
+                    if constexpr (SPS == 2) ex[g][i >> 1] |= ((e >> 8) & 0xFFFFu) << (16 * (i & 1));
+                    else ex[g][i >> 2] |= ((e >> 8) & 0xFFu) << (8 * (i & 3));
+                }
+            }
+        });
+    }
+};
+
+template <int SPS, int G>
+__global__ __launch_bounds__(kDecBlock) void decode_kernel(
+    const uint32_t* __restrict__ comp, int64_t words, const int64_t* __restrict__ off,
+    const uint16_t* __restrict__ st, const v2u* __restrict__ sm,
+    const v2u* __restrict__ table, int64_t K, int64_t N, uint8_t* __restrict__ out) {
+    constexpr uint32_t L = Alpha<SPS>::L;
+    __shared__ DecSmem<SPS, G> smem;
+    v2u* tbl = smem.tbl;
+    load_table<L>(tbl, table);
+    if (threadIdx.x == 0) smem.progress = 0;
+    __syncthreads();
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
+    const int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
+    if (g0 * kLanes >= K) return;
+    const int64_t n_groups = (K + kLanes - 1) / kLanes;
+    const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * G;
+    DecodeWave<SPS, G> w;
+    w.progress = &smem.progress;
+    w.live = (uint32_t)(wg_groups >= (int64_t)kDecWaves * G ? kDecWaves : (wg_groups + G - 1) / G);
+    w.lane = lane;
+    w.K = K;
+    w.N = N;
+    w.n_tiles = (int)((N + kTile - 1) / kTile);
+    w.tbl = tbl;
+    w.sm_stride = K * 8;
+    const int64_t t1 = w.n_tiles > 1 ? 1 : 0;
+    const int64_t t2 = w.n_tiles > 2 ? 2 : w.n_tiles - 1;
+    #pragma unroll
+    for (int j = 0; j < G; j++) {
+        const int64_t g = g0 + j < n_groups ? g0 + j : n_groups - 1;
+        const int64_t k0 = g * kLanes;
+        const int lanes = g0 + j < n_groups ? (K - k0 < kLanes ? (int)(K - k0) : kLanes) : 0;
+        w.active[j] = lane < lanes;
+        const uint32_t lane_ld = (uint32_t)(w.active[j] ? lane : (lanes ? lanes - 1 : 0));
+        w.sm_bytes[j] = (uint32_t)lanes * 8u;
+        w.out[j] = out + k0;
+        feed_init(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], lane, w.ch.p[j]);
+        lane_init(w.ch.l[j], w.active[j], st[k0 + lane_ld], L);
+        const char* row = reinterpret_cast<const char*>(sm + k0);
+        w.sm[j][0] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(row, w.sm_bytes[j]),
+                                                          (uint32_t)lane * 8u, 0, kNT);
+        w.sm[j][1] = __builtin_amdgcn_raw_buffer_load_b64(
+            rsrc(row + t1 * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+        w.pf[j] = row + t2 * w.sm_stride;
+    }
+    int t = 0;
+    for (; t + 2 <= w.n_tiles; t += 2) {
+        w.template tile<0>(t);
+        w.template tile<1>(t + 1);
+    }
+    if (t < w.n_tiles) w.template tile<0>(t);
 }
 
 int fail(int code, const std::string& msg) {
@@ -445,6 +710,10 @@ int sps_for(int32_t log2L) {
     return log2L == TANS_PAIR_LOG2L ? 2 : (log2L == TANS_NIBBLE_LOG2L ? 1 : 0);
 }
 
+template <int SPS>
+constexpr int kFusedGroups = 1;   // groups per wave in the fused kernel
+constexpr int kDecodeGroups = 2;   // groups per wave in the standalone decoder
+
 }  // namespace
 
 extern "C" {
@@ -453,7 +722,7 @@ int tans_fp8_memcpy(const void* a, void* c, int64_t n, void* stream) {
     if (n < 0 || n % 16 || ((!a || !c) && n)) return fail(TANS_EINVAL, "memcpy: n must be a multiple of 16");
     if (n == 0) return TANS_OK;
     const int64_t n_vec = n / 16;
-    const int64_t blocks = (n_vec + (int64_t)kBlock * kUnroll - 1) / ((int64_t)kBlock * kUnroll);
+    const int64_t blocks = (n_vec + kBlock - 1) / kBlock;
     hipLaunchKernelGGL(fp8_copy_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream,
                        (const v4u*)a, (v4u*)c, n_vec);
     return hip_check(hipGetLastError(), "fp8_copy_kernel launch");
@@ -463,7 +732,7 @@ int tans_fp8_vecadd_raw(const void* a, const void* b, void* c, int64_t n, void* 
     if (n < 0 || n % 16 || ((!a || !b || !c) && n)) return fail(TANS_EINVAL, "vecadd_raw: n must be a multiple of 16");
     if (n == 0) return TANS_OK;
     const int64_t n_vec = n / 16;
-    const int64_t blocks = (n_vec + (int64_t)kBlock * kUnroll - 1) / ((int64_t)kBlock * kUnroll);
+    const int64_t blocks = (n_vec + kBlock - 1) / kBlock;
     hipLaunchKernelGGL(fp8_add_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream,
                        (const v4u*)a, (const v4u*)b, (v4u*)c, n_vec);
     return hip_check(hipGetLastError(), "fp8_add_kernel launch");
@@ -475,7 +744,7 @@ int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs, 
     if (!((nsym == 256 && log2L == TANS_PAIR_LOG2L) || (nsym == 16 && log2L == TANS_NIBBLE_LOG2L)))
         return fail(TANS_EINVAL, "table: need (nsym 256, log2L 12) or (nsym 16, log2L 11)");
     hipLaunchKernelGGL(table_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, spread, freqs,
-                       (int)nsym, (int)log2L, (uint2*)table);
+                       (int)nsym, (int)log2L, (v2u*)table);
     return hip_check(hipGetLastError(), "table_kernel launch");
 }
 
@@ -491,18 +760,20 @@ int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes, const int64_
     if (!a_comp || !a_offsets || !a_states || !a_sm || !b_comp || !b_offsets || !b_states || !b_sm ||
         !table || !out)
         return fail(TANS_EINVAL, "vecadd_fused: null pointer");
-    if (a_comp_bytes % 16 || b_comp_bytes % 16 || a_comp_bytes < kSegWords * 4 ||
-        b_comp_bytes < kSegWords * 4)
-        return fail(TANS_EINVAL, "vecadd_fused: compressed buffers must be >= 1 KiB and 16-byte multiples");
+    if (a_comp_bytes < 0 || b_comp_bytes < 0 || a_comp_bytes % 4 || b_comp_bytes % 4)
+        return fail(TANS_EINVAL, "vecadd_fused: compressed sizes must be multiples of 4 bytes");
+    if (N / kTile > INT32_MAX) return fail(TANS_EINVAL, "vecadd_fused: N too large");
     const int64_t groups = (K + kLanes - 1) / kLanes;
-    const int64_t blocks = (groups + kWaves - 1) / kWaves;
-    const int64_t n_tiles = N / kTile;
+    const int64_t per_block = (int64_t)kDecWaves * (sps == 2 ? kFusedGroups<2> : kFusedGroups<1>);
+    const int64_t blocks = (groups + per_block - 1) / per_block;
+    if (blocks > INT32_MAX) return fail(TANS_EINVAL, "vecadd_fused: K too large");
+    const int n_tiles = (int)(N / kTile);
 #define TANS_LAUNCH_FUSED(S)                                                                      \
-    hipLaunchKernelGGL(fused_add_kernel<S>, dim3((unsigned)blocks), dim3(kDecBlock), 0,         \
-                       (hipStream_t)stream, (const uint32_t*)a_comp, a_comp_bytes / 4,          \
-                       a_offsets, a_states, (const uint2*)a_sm, (const uint32_t*)b_comp,        \
-                       b_comp_bytes / 4, b_offsets, b_states, (const uint2*)b_sm,               \
-                       (const uint2*)table, K, n_tiles, (v4u*)out)
+    hipLaunchKernelGGL((fused_add_kernel<S, kFusedGroups<S>>), dim3((unsigned)blocks),              \
+                       dim3(kDecBlock), 0, (hipStream_t)stream, (const uint32_t*)a_comp,         \
+                       a_comp_bytes / 4, a_offsets, a_states, (const v2u*)a_sm,                  \
+                       (const uint32_t*)b_comp, b_comp_bytes / 4, b_offsets, b_states,           \
+                       (const v2u*)b_sm, (const v2u*)table, K, n_tiles, (v4u*)out)
     if (sps == 2) TANS_LAUNCH_FUSED(2);
     else TANS_LAUNCH_FUSED(1);
 #undef TANS_LAUNCH_FUSED
@@ -518,14 +789,18 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
     if (K == 0 || N == 0) return TANS_OK;
     if (!comp || !offsets || !states || !sm || !table || !out)
         return fail(TANS_EINVAL, "decode: null pointer");
-    if (comp_bytes % 16 || comp_bytes < kSegWords * 4)
-        return fail(TANS_EINVAL, "decode: compressed buffer must be >= 1 KiB and a 16-byte multiple");
+    if (comp_bytes < 0 || comp_bytes % 4)
+        return fail(TANS_EINVAL, "decode: compressed size must be a multiple of 4 bytes");
+    if ((N + kTile - 1) / kTile > INT32_MAX) return fail(TANS_EINVAL, "decode: N too large");
     const int64_t groups = (K + kLanes - 1) / kLanes;
-    const int64_t blocks = (groups + kWaves - 1) / kWaves;
+    const int64_t per_block = (int64_t)kDecWaves * kDecodeGroups;
+    const int64_t blocks = (groups + per_block - 1) / per_block;
+    if (blocks > INT32_MAX) return fail(TANS_EINVAL, "decode: K too large");
 #define TANS_LAUNCH_DECODE(S)                                                                     \
-    hipLaunchKernelGGL(decode_kernel<S>, dim3((unsigned)blocks), dim3(kDecBlock), 0,            \
-                       (hipStream_t)stream, (const uint32_t*)comp, comp_bytes / 4, offsets,     \
-                       states, (const uint2*)sm, (const uint2*)table, K, N, (uint8_t*)out)
+    hipLaunchKernelGGL((decode_kernel<S, kDecodeGroups>), dim3((unsigned)blocks),                \
+                       dim3(kDecBlock), 0, (hipStream_t)stream, (const uint32_t*)comp,           \
+                       comp_bytes / 4, offsets, states, (const v2u*)sm, (const v2u*)table, K, N, \
+                       (uint8_t*)out)
     if (sps == 2) TANS_LAUNCH_DECODE(2);
     else TANS_LAUNCH_DECODE(1);
 #undef TANS_LAUNCH_DECODE
