@@ -1,21 +1,25 @@
 """Benchmark: fused tANS FP8 vecadd vs the raw FP8 vecadd on one MI355X.
 
 Workload: a and b are 2^29 E4M3FN elements each, drawn
-N(0, 0.02), scaled per tensor so |max| -> 448 and RNE-cast; one decode table
-from the joint a+b exponent histogram.  A "step" is one fused decode+add of
-the full 2^29-element pair into a 512 MiB output, inputs resident in HBM.
-The headline stream length is 64Ki elements per tANS stream (a 64-lane
-group, 1024 elements per lane, pair alphabet); the sweep over 1Ki/4Ki/16Ki
-streams and the nibble alphabet is reported beside it.
+N(0, 0.02) from a seed, scaled per tensor so |max| -> 448 and RNE-cast; one
+decode table from the joint a+b exponent histogram.  A "step" is one call of
+the drop-in API fp8_vecadd_fused_tans over the full 2^29-element pair into a
+512 MiB tiled output, with the encoded inputs resident in HBM.  The headline
+stream length is 64Ki elements per tANS stream (a 64-lane group, 1024
+elements per lane) with the pair alphabet; the 1Ki/4Ki/16Ki streams and the
+16-symbol nibble alphabet are reported beside it (reference
+bench_vecadd.py:102-165 sweeps the same way).
 
 Prints ONE JSON line (progress goes to stderr):
-  value        effective uncompressed GB/s = 3 * 2^29 / t_step
-  x_raw        t_raw / t_fused
-  roofline     algorithmic HBM bytes of one fused launch / its duration
-  cpu_baseline the reference's CPU path (C restatement, oracle/) on a
-               bounded sample of the same workload
+  value         effective uncompressed GB/s = 3 * 2^29 / t_step
+  x_raw         t_raw / t_fused (kernel durations)
+  roofline      compressed HBM bytes of one fused launch / its duration
+                (HIP events around each launch on the launch stream)
+  cpu_baseline  the reference's CPU path (the C restatement in oracle/) on a
+                bounded sample of the same workload
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+    python bench.py --profile fused|raw|memcpy|decode --steps 5   # for rocprofv3
 """
 from __future__ import annotations
 
@@ -23,6 +27,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import sys
 import time
 
@@ -34,6 +39,7 @@ HBM_PEAK_GBS = 8000.0
 N_ELEMS = 1 << 29
 HEADLINE_LANE = 1024                 # 64Ki-element streams
 SWEEP_LANES = (16, 64, 256, 1024)    # 1Ki, 4Ki, 16Ki, 64Ki streams
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fused_vecadd_64ki_pair_traffic.txt")
 
 
 def log(msg: str) -> None:
@@ -48,30 +54,41 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-sweep", action="store_true", help="headline config only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "traffic.json"),
-                   help="rocprof-derived HBM traffic per launch (JSON), if present")
+    p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode"),
+                   help="only launch this kernel --steps times (for rocprofv3)")
     return p.parse_args()
 
 
-def time_steps(fn, steps: int, warmup: int) -> float:
-    """Average ms per call, HIP events on the current (launch) stream."""
+def timed(fn, steps: int, warmup: int):
+    """(kernel ms, step ms): the average duration of one launch from HIP events
+    recorded around it on the launch stream, and the average time per call of
+    the whole loop (events around the loop)."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for s, e in ev:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    kernel = sum(s.elapsed_time(e) for s, e in ev) / steps
+    loop0 = torch.cuda.Event(enable_timing=True)
+    loop1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    loop0.record()
     for _ in range(steps):
         fn()
-    stop.record()
+    loop1.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps
+    return kernel, loop0.elapsed_time(loop1) / steps
 
 
 def make_inputs(seed: int):
-    """Config-1 vectors, generated on the GPU (seeded), returned on the CPU
-    for the encoder together with the joint exponent histogram."""
+    """Config-1 vectors, generated on the GPU from a seed, and the joint
+    exponent histogram."""
     import torch
     from rans_vectoradd import data as D
 
@@ -80,17 +97,15 @@ def make_inputs(seed: int):
         g = torch.Generator(device="cuda").manual_seed(s)
         x = torch.randn(N_ELEMS, generator=g, device="cuda") * 0.02
         q = (x * (D.E4M3_MAX / x.abs().max())).clamp_(-D.E4M3_MAX, D.E4M3_MAX)
-        q = q.to(torch.float8_e4m3fn).view(torch.uint8)
+        out.append(q.to(torch.float8_e4m3fn).view(torch.uint8))
         del x
-        out.append(q)
     hist = D.exp_histogram(torch.cat(out)).cpu()
     return out[0], out[1], hist
 
 
-def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps: int,
-                     warmup: int) -> dict:
-    import torch
-    import rans_vectoradd as R
+def encode_pair(qa_d, qb_d, hist, lane: int, alphabet: str):
+    """Encode a and b on the CPU; returns the device argument list of
+    fp8_vecadd_fused_tans, the compressed byte count and the encode time."""
     from rans_vectoradd import tans_codec as T
 
     K = N_ELEMS // lane
@@ -102,25 +117,55 @@ def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps:
     order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
     args = [x.cuda() for x in (*[ea[i] for i in order], *[eb[i] for i in order], tbl)]
     in_bytes = T.compressed_bytes(*ea[:5]) + T.compressed_bytes(*eb[:5])
+    return args, in_bytes, t_enc
+
+
+def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps: int,
+                     warmup: int) -> dict:
+    import torch
+    import rans_vectoradd as R
+
+    K = N_ELEMS // lane
+    args, in_bytes, t_enc = encode_pair(qa_d, qb_d, hist, lane, alphabet)
     hbm_bytes = in_bytes + N_ELEMS                       # + the output write
-    bits = in_bytes * 8 / (2 * N_ELEMS)
     fn = lambda: R.fp8_vecadd_fused_tans(*args, lane)    # noqa: E731
     out = fn()
     exact = bool(torch.equal(out.view(lane // 16, K, 16).permute(1, 0, 2).reshape(-1), raw_out))
-    ms = time_steps(fn, steps, warmup)
-    del args, out
+    del out
+    t0 = time.perf_counter()
+    for _ in range(10):
+        fn()
+    host_us = (time.perf_counter() - t0) / 10 * 1e6      # API call cost on the host
+    kernel_ms, step_ms = timed(fn, steps, warmup)
+    del args
     torch.cuda.empty_cache()
-    return {"stream_elems": 64 * lane, "lane_elems": lane, "alphabet": alphabet, "ms": ms,
-            "bits_per_byte": bits, "hbm_bytes": hbm_bytes, "encode_s": t_enc,
-            "exact_vs_raw": exact, "eff_gbs": 3 * N_ELEMS / (ms * 1e-3) / 1e9,
-            "hbm_gbs": hbm_bytes / (ms * 1e-3) / 1e9}
+    return {"stream_elems": 64 * lane, "lane_elems": lane, "alphabet": alphabet,
+            "kernel_ms": kernel_ms, "step_ms": step_ms, "api_host_us": host_us,
+            "bits_per_byte": in_bytes * 8 / (2 * N_ELEMS), "hbm_bytes": hbm_bytes,
+            "encode_s": t_enc, "exact_vs_raw": exact,
+            "eff_gbs": 3 * N_ELEMS / (step_ms * 1e-3) / 1e9,
+            "hbm_gbs": hbm_bytes / (kernel_ms * 1e-3) / 1e9}
+
+
+def read_traffic():
+    """HBM bytes per fused launch measured with rocprofv3 (FETCH_SIZE and
+    WRITE_SIZE, scaled by the copy-kernel calibration), from the committed
+    summary; None if it is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            m = re.search(r"^bytes_per_launch:\s*(\d+)", f.read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def cpu_baseline(seed: int) -> dict:
-    """The reference's CPU path, restated in C (oracle/): pair alphabet,
-    L = 4096, 128-stream blocks; encode then decode+add.  Bounded sample:
-    2^25 elements per vector, 1024 elements per stream, decode+add repeated
-    for about 10 s."""
+    """The reference's CPU path restated in C (oracle/): pair alphabet,
+    L = 4096, 128-stream slab blocks (csrc/tans_codec.cpp; decode
+    csrc/tans_decode.cu:65-155 + add csrc/vecadd.cu:27-39, which only exist
+    as GPU kernels in the reference).  Bounded sample: 2^25 elements per
+    vector, 1024 elements per stream; encode both, then decode+add repeated
+    for about 10 s on all host cores."""
     import numpy as np
     import torch
     from oracle import oracle as O
@@ -166,18 +211,49 @@ def cpu_baseline(seed: int) -> dict:
         pass
     per = t_dec / reps
     return {"value": 3 * n / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"2^25 elements per vector (1024 per stream), decode+add x{reps}; "
-                      f"encode of both vectors {t_enc:.2f} s",
-            "encode_s": t_enc, "decode_add_s": per, "exact": bool(np.array_equal(got, ref)),
-            "cpu_model": cpu}
+            "sample": f"2^25 elements per vector (1024 per stream), decode+add x{reps} "
+                      f"(~10 s); encode of both vectors {t_enc:.2f} s",
+            "encode_s": t_enc, "encode_gbs": 2 * n / t_enc / 1e9, "decode_add_s": per,
+            "exact": bool(np.array_equal(got, ref)), "cpu_model": cpu}
+
+
+def profile_only(args) -> None:
+    """Launch one kernel --steps times (after --warmup) with nothing else in
+    the timed part, for rocprofv3 runs."""
+    import torch
+    import rans_vectoradd as R
+    from rans_vectoradd import tans_codec as T
+
+    qa, qb, hist = make_inputs(args.seed)
+    if args.profile == "raw":
+        fn = lambda: R.fp8_vecadd_raw(qa, qb)   # noqa: E731
+    elif args.profile == "memcpy":
+        fn = lambda: R.fp8_memcpy(qa)           # noqa: E731
+    elif args.profile == "fused":
+        dev_args, _, _ = encode_pair(qa, qb, hist, HEADLINE_LANE, "pair")
+        fn = lambda: R.fp8_vecadd_fused_tans(*dev_args, HEADLINE_LANE)   # noqa: E731
+    else:
+        K = N_ELEMS // HEADLINE_LANE
+        e = T.encode(qa.cpu().reshape(K, HEADLINE_LANE), hist, alphabet="pair")
+        d = [x.cuda() for x in e]
+        fn = lambda: R.gpu_tans_decode(d[0], d[2], d[1], d[3], d[4], d[6], d[5], HEADLINE_LANE)  # noqa
+    log(f"profile {args.profile}: {args.warmup} warm-up + {args.steps} launches")
+    for _ in range(args.warmup + args.steps):
+        fn()
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": args.profile, "launches": args.warmup + args.steps}))
 
 
 def main() -> None:
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
+        print(json.dumps({"error": "this build measures one GPU: the path has no cross-GPU "
+                                   "step (see DESIGN.md on sharding); run with --gpus 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.profile:
+        profile_only(args)
+        return
     import torch
     import rans_vectoradd as R
 
@@ -185,8 +261,8 @@ def main() -> None:
     qa, qb, hist = make_inputs(args.seed)
     log("raw and memcpy timing")
     raw_out = R.fp8_vecadd_raw(qa, qb)
-    ms_raw = time_steps(lambda: R.fp8_vecadd_raw(qa, qb), args.steps, args.warmup)
-    ms_cpy = time_steps(lambda: R.fp8_memcpy(qa), args.steps, args.warmup)
+    raw_kernel, raw_step = timed(lambda: R.fp8_vecadd_raw(qa, qb), args.steps, args.warmup)
+    cpy_kernel, _ = timed(lambda: R.fp8_memcpy(qa), args.steps, args.warmup)
 
     configs = [(HEADLINE_LANE, "pair")]
     if not args.no_sweep:
@@ -195,26 +271,21 @@ def main() -> None:
     results = []
     for lane, alph in configs:
         log(f"fused: stream {64 * lane} elements ({lane} per lane), {alph}")
-        results.append(run_fused_config(qa, qb, raw_out, hist, lane, alph, args.steps,
-                                        args.warmup))
-        r = results[-1]
-        log(f"  {r['ms']:.4f} ms  x_raw {ms_raw / r['ms']:.3f}  bits/B {r['bits_per_byte']:.3f}"
-            f"  exact {r['exact_vs_raw']}")
+        r = run_fused_config(qa, qb, raw_out, hist, lane, alph, args.steps, args.warmup)
+        results.append(r)
+        log(f"  kernel {r['kernel_ms'] * 1e3:.1f} us  step {r['step_ms'] * 1e3:.1f} us  "
+            f"x_raw {raw_kernel / r['kernel_ms']:.3f}  bits/B {r['bits_per_byte']:.3f}  "
+            f"exact {r['exact_vs_raw']}  api {r['api_host_us']:.0f} us")
     head = results[0]
-    ms = head["ms"]
-    traffic = None
-    if os.path.exists(args.traffic_file):
-        with open(args.traffic_file) as f:
-            traffic = json.load(f).get("fused_vecadd_bytes_per_launch")
-    achieved = head["hbm_bytes"] / (ms * 1e-3) / 1e9
+    achieved = head["hbm_bytes"] / (head["kernel_ms"] * 1e-3) / 1e9
     line = {
         "metric": "effective GB/s and x raw for fused tANS FP8 vecadd (1 GiB); bits/FP8 byte",
-        "value": 3 * N_ELEMS / (ms * 1e-3) / 1e9,
+        "value": 3 * N_ELEMS / (head["step_ms"] * 1e-3) / 1e9,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms,
+        "ms_per_step": head["step_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -224,18 +295,22 @@ def main() -> None:
                                "64Ki-element streams (64 lanes x 1024), pair alphabet",
                    "elements_per_vector": N_ELEMS, "stream_elems": head["stream_elems"],
                    "lane_elems": head["lane_elems"], "alphabet": head["alphabet"]},
-        "x_raw": ms_raw / ms,
+        "x_raw": raw_kernel / head["kernel_ms"],
         "bits_per_byte": head["bits_per_byte"],
         "exact_vs_raw": head["exact_vs_raw"],
+        "kernel_ms": head["kernel_ms"],
         "compressed_hbm_gbs": achieved,
-        "raw": {"ms": ms_raw, "gbs": 3 * N_ELEMS / (ms_raw * 1e-3) / 1e9,
-                "frac_of_peak": 3 * N_ELEMS / (ms_raw * 1e-3) / 1e9 / HBM_PEAK_GBS},
-        "memcpy": {"ms": ms_cpy, "gbs": 2 * N_ELEMS / (ms_cpy * 1e-3) / 1e9},
+        "raw": {"kernel_ms": raw_kernel, "step_ms": raw_step,
+                "gbs": 3 * N_ELEMS / (raw_kernel * 1e-3) / 1e9,
+                "frac_of_peak": 3 * N_ELEMS / (raw_kernel * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "memcpy": {"kernel_ms": cpy_kernel, "gbs": 2 * N_ELEMS / (cpy_kernel * 1e-3) / 1e9},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic},
-        "sweep": [{k: r[k] for k in ("stream_elems", "lane_elems", "alphabet", "ms",
-                                     "bits_per_byte", "eff_gbs", "hbm_gbs", "exact_vs_raw")}
-                  | {"x_raw": ms_raw / r["ms"]} for r in results],
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": read_traffic()},
+        "sweep": [{k: r[k] for k in ("stream_elems", "lane_elems", "alphabet", "kernel_ms",
+                                     "step_ms", "bits_per_byte", "eff_gbs", "hbm_gbs",
+                                     "exact_vs_raw")}
+                  | {"x_raw": raw_kernel / r["kernel_ms"]} for r in results],
     }
     del raw_out, qa, qb
     torch.cuda.empty_cache()

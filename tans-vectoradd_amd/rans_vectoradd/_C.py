@@ -17,6 +17,7 @@ Kernels run on the current torch stream of the inputs' device.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 
 import torch
@@ -33,12 +34,19 @@ __all__ = [
 ]
 
 
-def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
-    return ctypes.c_void_p(t.data_ptr())
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
 
 
-def _stream(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _on(device: torch.device):
+    """Make `device` current for the launch (a no-op when it already is)."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -47,9 +55,10 @@ def _require(cond: bool, msg: str) -> None:
 
 
 def _check_dev(name: str, t: torch.Tensor, dtype: torch.dtype) -> None:
-    _require(t.is_cuda, f"{name} must be CUDA")
-    _require(t.dtype == dtype, f"{name} must be {dtype}")
-    _require(t.is_contiguous(), f"{name} must be contiguous")
+    if not (t.is_cuda and t.dtype == dtype and t.is_contiguous()):
+        _require(t.is_cuda, f"{name} must be CUDA")
+        _require(t.dtype == dtype, f"{name} must be {dtype}")
+        _require(t.is_contiguous(), f"{name} must be contiguous")
 
 
 def _check_cpu(name: str, t: torch.Tensor, dtype: torch.dtype) -> None:
@@ -134,7 +143,7 @@ def gpu_tans_decode(compressed: torch.Tensor, offsets: torch.Tensor, states: tor
     out = torch.empty((N, K), dtype=torch.uint8, device=dev)
     if K == 0 or N == 0:
         return out
-    with torch.cuda.device(dev):
+    with _on(dev):
         table = torch.empty(2 << log2L, dtype=torch.int32, device=dev)
         stream = _stream(dev)
         check(lib.tans_build_decode_table_device(_ptr(spread), _ptr(freqs), nsym, log2L,
@@ -150,7 +159,7 @@ def fp8_memcpy(A: torch.Tensor) -> torch.Tensor:
     _check_dev("A", A, torch.uint8)
     _require(A.numel() % 16 == 0, "A length must be a multiple of 16")
     C = torch.empty_like(A)
-    with torch.cuda.device(A.device):
+    with _on(A.device):
         check(lib.tans_fp8_memcpy(_ptr(A), _ptr(C), A.numel(), _stream(A.device)), "fp8_memcpy")
     return C
 
@@ -163,7 +172,7 @@ def fp8_vecadd_raw(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     _require(A.numel() % 16 == 0, "A/B length must be a multiple of 16")
     _require(A.device == B.device, "A and B must be on the same device")
     C = torch.empty_like(A)
-    with torch.cuda.device(A.device):
+    with _on(A.device):
         check(lib.tans_fp8_vecadd_raw(_ptr(A), _ptr(B), _ptr(C), A.numel(), _stream(A.device)),
               "fp8_vecadd_raw")
     return C
@@ -199,7 +208,7 @@ def fp8_vecadd_fused_tans(a_comp: torch.Tensor, a_offsets: torch.Tensor, a_state
     out = torch.empty(K * N, dtype=torch.uint8, device=dev)
     if K == 0 or N == 0:
         return out
-    with torch.cuda.device(dev):
+    with _on(dev):
         check(lib.tans_fp8_vecadd_fused(_ptr(a_comp), a_comp.numel(), _ptr(a_offsets),
                                         _ptr(a_states), _ptr(a_sm), _ptr(b_comp), b_comp.numel(),
                                         _ptr(b_offsets), _ptr(b_states), _ptr(b_sm),
