@@ -18,7 +18,7 @@ Prints ONE JSON line (progress goes to stderr):
   cpu_baseline  the reference's CPU path (the C restatement in oracle/) on a
                 bounded sample of the same workload
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20]
     python bench.py --profile fused|raw|memcpy|decode --steps 5   # for rocprofv3
 """
 from __future__ import annotations
@@ -39,6 +39,7 @@ HBM_PEAK_GBS = 8000.0
 N_ELEMS = 1 << 29
 HEADLINE_LANE = 1024                 # 64Ki-element streams
 SWEEP_LANES = (16, 64, 256, 1024)    # 1Ki, 4Ki, 16Ki, 64Ki streams
+SETTLE_S = 0.3                       # seconds of back-to-back calls before timing
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fused_vecadd_64ki_pair_traffic.txt")
 
 
@@ -49,9 +50,11 @@ def log(msg: str) -> None:
 def parse_args() -> argparse.Namespace:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--settle", type=float, default=SETTLE_S,
+                   help="seconds of back-to-back calls before each timing (0: none)")
     p.add_argument("--no-sweep", action="store_true", help="headline config only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode"),
@@ -59,11 +62,31 @@ def parse_args() -> argparse.Namespace:
     return p.parse_args()
 
 
-def timed(fn, steps: int, warmup: int):
+def settle(fn, seconds: float) -> int:
+    """Call fn back to back for about `seconds` before anything is timed.
+
+    From idle, MI355X's power management needs some tens of launches of a
+    VALU-heavy kernel to reach its sustained clocks: the fused kernel's first
+    ~80 back-to-back launches run up to 1.5x slower than the steady state,
+    while the memory-bound raw kernel shows no such transient.  Timing starts
+    after this phase so every kernel is measured at its sustained rate."""
+    import torch
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn()
+        n += 20
+        torch.cuda.synchronize()
+    return n
+
+
+def timed(fn, steps: int, warmup: int, settle_s: float = SETTLE_S):
     """(kernel ms, step ms): the average duration of one launch from HIP events
     recorded around it on the launch stream, and the average time per call of
-    the whole loop (events around the loop)."""
+    the whole loop (events around the loop).  Both after settle() and
+    `warmup` untimed calls."""
     import torch
+    settle(fn, settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -121,7 +144,7 @@ def encode_pair(qa_d, qb_d, hist, lane: int, alphabet: str):
 
 
 def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps: int,
-                     warmup: int) -> dict:
+                     warmup: int, settle_s: float) -> dict:
     import torch
     import rans_vectoradd as R
 
@@ -136,7 +159,7 @@ def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps:
     for _ in range(10):
         fn()
     host_us = (time.perf_counter() - t0) / 10 * 1e6      # API call cost on the host
-    kernel_ms, step_ms = timed(fn, steps, warmup)
+    kernel_ms, step_ms = timed(fn, steps, warmup, settle_s)
     del args
     torch.cuda.empty_cache()
     return {"stream_elems": 64 * lane, "lane_elems": lane, "alphabet": alphabet,
@@ -237,11 +260,13 @@ def profile_only(args) -> None:
         e = T.encode(qa.cpu().reshape(K, HEADLINE_LANE), hist, alphabet="pair")
         d = [x.cuda() for x in e]
         fn = lambda: R.gpu_tans_decode(d[0], d[2], d[1], d[3], d[4], d[6], d[5], HEADLINE_LANE)  # noqa
-    log(f"profile {args.profile}: {args.warmup} warm-up + {args.steps} launches")
+    n = settle(fn, args.settle)
+    log(f"profile {args.profile}: {n} settle + {args.warmup} warm-up + {args.steps} launches")
     for _ in range(args.warmup + args.steps):
         fn()
     torch.cuda.synchronize()
-    print(json.dumps({"profile": args.profile, "launches": args.warmup + args.steps}))
+    print(json.dumps({"profile": args.profile, "settle": n,
+                      "launches": n + args.warmup + args.steps}))
 
 
 def main() -> None:
@@ -261,8 +286,9 @@ def main() -> None:
     qa, qb, hist = make_inputs(args.seed)
     log("raw and memcpy timing")
     raw_out = R.fp8_vecadd_raw(qa, qb)
-    raw_kernel, raw_step = timed(lambda: R.fp8_vecadd_raw(qa, qb), args.steps, args.warmup)
-    cpy_kernel, _ = timed(lambda: R.fp8_memcpy(qa), args.steps, args.warmup)
+    raw_kernel, raw_step = timed(lambda: R.fp8_vecadd_raw(qa, qb), args.steps, args.warmup,
+                                 args.settle)
+    cpy_kernel, _ = timed(lambda: R.fp8_memcpy(qa), args.steps, args.warmup, args.settle)
 
     configs = [(HEADLINE_LANE, "pair")]
     if not args.no_sweep:
@@ -271,7 +297,8 @@ def main() -> None:
     results = []
     for lane, alph in configs:
         log(f"fused: stream {64 * lane} elements ({lane} per lane), {alph}")
-        r = run_fused_config(qa, qb, raw_out, hist, lane, alph, args.steps, args.warmup)
+        r = run_fused_config(qa, qb, raw_out, hist, lane, alph, args.steps, args.warmup,
+                             args.settle)
         results.append(r)
         log(f"  kernel {r['kernel_ms'] * 1e3:.1f} us  step {r['step_ms'] * 1e3:.1f} us  "
             f"x_raw {raw_kernel / r['kernel_ms']:.3f}  bits/B {r['bits_per_byte']:.3f}  "
@@ -285,6 +312,7 @@ def main() -> None:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": args.settle,
         "ms_per_step": head["step_ms"],
         "higher_is_better": True,
         "scaling": "weak",
