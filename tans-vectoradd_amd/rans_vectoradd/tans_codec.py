@@ -47,7 +47,14 @@ def quantize_freqs(probs, target: int = M) -> np.ndarray:
     Same rule as the reference (tans_codec.py:30-46): round to nearest, give
     every p > 0 at least 1 and every p == 0 exactly 0, then move one unit at
     a time to (or from) the symbol whose rounding error is largest, lowest
-    index first on ties.  The result is a drop-in for the reference's."""
+    index first on ties.  The result is a drop-in for the reference's.
+
+    One deliberate difference: when the total is over target and every
+    shrinkable symbol is already under-served, the reference's argmax can
+    pick a zero-probability symbol (its error is 0) and return frequency -1,
+    which no spread can hold; that happens for the pair alphabet whenever an
+    exponent never occurs.  Zero-probability symbols are never shrunk here,
+    so the results agree wherever the reference's are valid."""
     p = np.asarray(probs, dtype=np.float64).reshape(-1)
     scaled = p * target
     f = np.where(p > 0, np.maximum(np.rint(scaled), 1.0), 0.0).astype(np.int64)
@@ -57,7 +64,7 @@ def quantize_freqs(probs, target: int = M) -> np.ndarray:
         f[int(np.argmax(gain))] += 1
         short -= 1
     while short < 0:                       # over target: shrink most over-served
-        excess = np.where((p > 0) & (f <= 1), -np.inf, f - scaled)
+        excess = np.where((p == 0) | (f <= 1), -np.inf, f - scaled)
         f[int(np.argmax(excess))] -= 1
         short += 1
     if int(f.sum()) != target:

@@ -35,9 +35,21 @@ def _encode_check(T, fp8, exp_freqs, alphabet):
 
 def test_quantize_freqs_matches_reference_golden(T):
     assert np.array_equal(T.quantize_freqs(GOLDEN["qf_pair_qwen_in"], 4096), GOLDEN["qf_pair_qwen_out"])
+    invalid = 0
     for i in range(7):
-        got = T.quantize_freqs(GOLDEN[f"qf_case{i}_in"], target=int(GOLDEN[f"qf_case{i}_target"][0]))
-        assert np.array_equal(got, GOLDEN[f"qf_case{i}_out"]), f"case {i}"
+        probs = GOLDEN[f"qf_case{i}_in"]
+        want = GOLDEN[f"qf_case{i}_out"]
+        tgt = int(GOLDEN[f"qf_case{i}_target"][0])
+        got = T.quantize_freqs(probs, target=tgt)
+        if want.min() >= 0:
+            assert np.array_equal(got, want), f"case {i}"
+        else:
+            # the reference returned a negative frequency for a p == 0
+            # symbol; the product keeps it at 0 and shrinks a live symbol
+            invalid += 1
+            assert got.sum() == tgt and np.array_equal(got == 0, probs == 0), f"case {i}"
+            assert (got[probs > 0] >= 1).all()
+    assert invalid == 1                     # golden case 3
 
 
 @pytest.mark.parametrize("alphabet", list(ALPHABETS))
@@ -51,6 +63,40 @@ def test_symbol_freqs_and_spread_match_oracle(T, alphabet):
         p = (p[:, None] * p[None, :]).reshape(-1)
     assert np.array_equal(f, O.quantize_freqs(p, L))
     assert np.array_equal(T.build_spread(f), O.build_spread(f, L))
+
+
+def test_absent_exponent_gives_valid_pair_table(T):
+    """An exponent that never occurs makes 31 pair symbols impossible.  The
+    reference's fix-up rule can then shrink one of them to -1 (the oracle,
+    restating it, does); the product never shrinks a zero-probability
+    symbol, and agrees with the oracle whenever the oracle's result is
+    valid."""
+    from rans_vectoradd import data as D
+    torch.manual_seed(3)
+    fp8 = D.random_fp8_bytes(64 * 256, device="cpu")
+    e = (fp8 >> 3) & 0xF
+    fp8 = torch.where(e == 0, fp8 | (1 << 3), fp8)          # exponent 0 -> 1
+    hist = D.exp_histogram(fp8)
+    assert hist[0] == 0
+    p = hist.numpy().astype(np.float32)
+    p = p / p.sum()
+    pp = (p[:, None] * p[None, :]).reshape(-1)
+    ref = O.quantize_freqs(pp, 4096)
+    got = T.symbol_freqs(hist, "pair")
+    assert got.sum() == 4096 and got.min() >= 0
+    assert np.array_equal(got == 0, pp == 0)
+    if ref.min() >= 0:
+        assert np.array_equal(got, ref)
+    else:                                   # the reference's rule failed here
+        assert np.array_equal(got[pp > 0] >= 1, np.ones((pp > 0).sum(), bool))
+    _encode_check(T, fp8.reshape(64, 256), hist, "pair")
+    # cases where the reference's result is valid are unchanged
+    for i in range(7):
+        probs = GOLDEN[f"qf_case{i}_in"]
+        tgt = int(GOLDEN[f"qf_case{i}_target"][0])
+        ref_i = O.quantize_freqs(probs, tgt)
+        if ref_i.min() >= 0:
+            assert np.array_equal(T.quantize_freqs(probs, tgt), ref_i)
 
 
 @pytest.mark.parametrize("alphabet", list(ALPHABETS))
