@@ -15,11 +15,14 @@ Prints ONE JSON line (progress goes to stderr):
   x_raw         t_raw / t_fused (kernel durations)
   roofline      compressed HBM bytes of one fused launch / its duration
                 (HIP events around each launch on the launch stream)
+  decode        config 2: gpu_tans_decode of 2^30 elements (Gaussian and
+                Laplace data, nibble and pair tables), GB/s and bits/byte
   cpu_baseline  the reference's CPU path (the C restatement in oracle/) on a
                 bounded sample of the same workload
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
-    python bench.py --profile fused|raw|memcpy|decode --steps 5   # for rocprofv3
+    python bench.py --profile fused|raw|memcpy|decode [--alphabet pair|nibble] --steps 5
+                                  # one kernel only, for rocprofv3
 """
 from __future__ import annotations
 
@@ -38,6 +41,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 N_ELEMS = 1 << 29
 HEADLINE_LANE = 1024                 # 64Ki-element streams
+DECODE_ELEMS = 1 << 30               # config 2
 SWEEP_LANES = (16, 64, 256, 1024)    # 1Ki, 4Ki, 16Ki, 64Ki streams
 SETTLE_S = 0.3                       # seconds of back-to-back calls before timing
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fused_vecadd_64ki_pair_traffic.txt")
@@ -57,6 +61,9 @@ def parse_args() -> argparse.Namespace:
                    help="seconds of back-to-back calls before each timing (0: none)")
     p.add_argument("--no-sweep", action="store_true", help="headline config only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-decode", action="store_true", help="skip config 2 (standalone decode)")
+    p.add_argument("--alphabet", choices=("pair", "nibble"), default="pair",
+                   help="alphabet of --profile fused/decode")
     p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode"),
                    help="only launch this kernel --steps times (for rocprofv3)")
     return p.parse_args()
@@ -170,6 +177,40 @@ def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps:
             "hbm_gbs": hbm_bytes / (kernel_ms * 1e-3) / 1e9}
 
 
+def run_decode_config(dist: str, alphabet: str, seed: int, steps: int, warmup: int,
+                      settle_s: float) -> dict:
+    """Config 2: gpu_tans_decode of 2^30 E4M3FN elements (1024 per lane)
+    back to FP8 bytes [N, K]; the table is built from the data's own
+    histogram; bit-exact round trip checked."""
+    import torch
+    import rans_vectoradd as R
+    from rans_vectoradd import data as D, tans_codec as T
+
+    n, lane = DECODE_ELEMS, HEADLINE_LANE
+    K = n // lane
+    gen = D.gaussian_fp8_bytes if dist == "gaussian" else D.laplace_fp8_bytes
+    q, _ = gen(n, seed=seed, device="cuda")
+    hist = D.exp_histogram(q).cpu()
+    t0 = time.perf_counter()
+    e = T.encode(q.cpu().reshape(K, lane), hist, alphabet=alphabet)
+    t_enc = time.perf_counter() - t0
+    in_bytes = T.compressed_bytes(*e[:5])
+    comp, st, off, part, sm, fr, sp = [x.cuda() for x in e]
+    del e
+    fn = lambda: R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, lane)   # noqa: E731
+    out = fn()
+    exact = bool(torch.equal(out, q.view(K, lane).t()))
+    del out, q
+    kernel_ms, step_ms = timed(fn, steps, warmup, settle_s)
+    del comp, st, off, part, sm, fr, sp
+    torch.cuda.empty_cache()
+    return {"dist": dist, "alphabet": alphabet, "elements": n, "lane_elems": lane,
+            "bits_per_byte": in_bytes * 8 / n, "exact": exact, "encode_s": t_enc,
+            "call_ms": kernel_ms, "step_ms": step_ms,
+            "eff_gbs": 2 * n / (step_ms * 1e-3) / 1e9,
+            "hbm_gbs": (in_bytes + n) / (step_ms * 1e-3) / 1e9}
+
+
 def read_traffic():
     """HBM bytes per fused launch measured with rocprofv3 (FETCH_SIZE and
     WRITE_SIZE, scaled by the copy-kernel calibration), from the committed
@@ -247,19 +288,24 @@ def profile_only(args) -> None:
     import rans_vectoradd as R
     from rans_vectoradd import tans_codec as T
 
-    qa, qb, hist = make_inputs(args.seed)
-    if args.profile == "raw":
-        fn = lambda: R.fp8_vecadd_raw(qa, qb)   # noqa: E731
-    elif args.profile == "memcpy":
-        fn = lambda: R.fp8_memcpy(qa)           # noqa: E731
-    elif args.profile == "fused":
-        dev_args, _, _ = encode_pair(qa, qb, hist, HEADLINE_LANE, "pair")
-        fn = lambda: R.fp8_vecadd_fused_tans(*dev_args, HEADLINE_LANE)   # noqa: E731
-    else:
-        K = N_ELEMS // HEADLINE_LANE
-        e = T.encode(qa.cpu().reshape(K, HEADLINE_LANE), hist, alphabet="pair")
+    if args.profile == "decode":   # config 2: 2^30 Gaussian elements, 1024 per lane
+        from rans_vectoradd import data as D
+        K = DECODE_ELEMS // HEADLINE_LANE
+        q, _ = D.gaussian_fp8_bytes(DECODE_ELEMS, seed=args.seed, device="cuda")
+        e = T.encode(q.cpu().reshape(K, HEADLINE_LANE), D.exp_histogram(q).cpu(),
+                     alphabet=args.alphabet)
+        del q
         d = [x.cuda() for x in e]
         fn = lambda: R.gpu_tans_decode(d[0], d[2], d[1], d[3], d[4], d[6], d[5], HEADLINE_LANE)  # noqa
+    else:
+        qa, qb, hist = make_inputs(args.seed)
+        if args.profile == "raw":
+            fn = lambda: R.fp8_vecadd_raw(qa, qb)   # noqa: E731
+        elif args.profile == "memcpy":
+            fn = lambda: R.fp8_memcpy(qa)           # noqa: E731
+        else:
+            dev_args, _, _ = encode_pair(qa, qb, hist, HEADLINE_LANE, args.alphabet)
+            fn = lambda: R.fp8_vecadd_fused_tans(*dev_args, HEADLINE_LANE)   # noqa: E731
     n = settle(fn, args.settle)
     log(f"profile {args.profile}: {n} settle + {args.warmup} warm-up + {args.steps} launches")
     for _ in range(args.warmup + args.steps):
@@ -342,6 +388,16 @@ def main() -> None:
     }
     del raw_out, qa, qb
     torch.cuda.empty_cache()
+    if not args.no_decode:
+        line["decode"] = []
+        for dist in ("gaussian", "laplace"):
+            for alph in ("nibble", "pair"):
+                log(f"decode: 2^30 {dist}, {alph}")
+                r = run_decode_config(dist, alph, args.seed, args.steps, args.warmup, args.settle)
+                line["decode"].append(r)
+                log(f"  call {r['step_ms'] * 1e3:.1f} us  eff {r['eff_gbs']:.0f} GB/s  "
+                    f"hbm {r['hbm_gbs']:.0f} GB/s  bits/B {r['bits_per_byte']:.3f}  "
+                    f"exact {r['exact']}")
     if not args.no_cpu:
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.seed)

@@ -129,27 +129,68 @@ __global__ __launch_bounds__(kBlock) void fp8_add_kernel(const v4u* __restrict__
 }
 
 // ---------------------------------------------------------------------
-// Decode table on the device.  One workgroup; thread s owns symbol s and
-// walks the spread in slot order to number its occurrences.
+// Decode table on the device: one workgroup of 16 waves, wave w owning
+// slots [w L/16, (w+1) L/16) in rounds of 64.  A symbol's rank (its earlier
+// slots in slot order) is its count in earlier waves plus its count earlier
+// in its own wave; the latter is found per round by taking the distinct
+// symbols of the round one at a time (ballot of the lanes holding the
+// first remaining one, mbcnt for each lane's place among them).
 // ---------------------------------------------------------------------
-__global__ __launch_bounds__(256) void table_kernel(const int32_t* __restrict__ spread,
-                                                    const int32_t* __restrict__ freqs, int nsym,
-                                                    int log2L, v2u* __restrict__ table) {
-    __shared__ int32_t sp[1 << TANS_PAIR_LOG2L];
+constexpr int kTableWaves = 16;
+
+__global__ __launch_bounds__(kTableWaves * 64) void table_kernel(
+    const int32_t* __restrict__ spread, const int32_t* __restrict__ freqs, int nsym, int log2L,
+    v2u* __restrict__ table) {
+    __shared__ uint32_t cnt[kTableWaves][256];   // occurrences per wave, then per earlier waves
     const uint32_t L = 1u << log2L;
-    for (uint32_t i = threadIdx.x; i < L; i += blockDim.x) sp[i] = spread[i];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    for (uint32_t i = threadIdx.x; i < kTableWaves * 256; i += blockDim.x) (&cnt[0][0])[i] = 0;
     __syncthreads();
-    const int s = threadIdx.x;
-    if (s >= nsym) return;
-    const uint32_t f = (uint32_t)freqs[s];
-    const uint32_t ex = (nsym == 256) ? ((((uint32_t)s >> 4) << 11) | (((uint32_t)s & 0xFu) << 19))
-                                      : ((uint32_t)s << 11);
-    uint32_t rank = 0;
-    for (uint32_t slot = 0; slot < L; slot++) {
-        if (sp[slot] != s) continue;
-        const uint32_t xp = f + rank++;
-        const int nb = xp ? log2L - (31 - __builtin_clz(xp)) : 0;
+    const uint32_t per_wave = L / kTableWaves;      // 256 (pair) or 128 (nibble) slots
+    const int rounds = (int)(per_wave / 64);
+    uint32_t sym[4] = {0u, 0u, 0u, 0u}, rank[4] = {0u, 0u, 0u, 0u};
+    #pragma unroll
+    for (int r = 0; r < 4; r++) {
+        if (r >= rounds) break;
+        const uint32_t slot = wave * per_wave + (uint32_t)r * 64 + lane;
+        // a symbol outside the alphabet is folded into it: a wrong table,
+        // never an out-of-range access (the host builder rejects such input)
+        const uint32_t s = (uint32_t)spread[slot] & (uint32_t)(nsym - 1);
+        sym[r] = s;
+        uint64_t todo = __ballot(true);
+        while (todo) {   // wave-uniform
+            const uint32_t first = (uint32_t)__builtin_ctzll(todo);
+            const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)s, (int)first);
+            const uint64_t m = __ballot(s == s0);
+            const uint32_t before = cnt[wave][s0];
+            if (s == s0)
+                rank[r] = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            if (lane == (int)first) cnt[wave][s0] = before + (uint32_t)__popcll(m);
+            todo &= ~m;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < (unsigned)nsym) {            // exclusive prefix over the waves
+        uint32_t run = 0;
+        for (int w = 0; w < kTableWaves; w++) {
+            const uint32_t c = cnt[w][threadIdx.x];
+            cnt[w][threadIdx.x] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    #pragma unroll
+    for (int r = 0; r < 4; r++) {
+        if (r >= rounds) break;
+        const uint32_t s = sym[r];
+        const uint32_t slot = wave * per_wave + (uint32_t)r * 64 + lane;
+        const uint32_t xp = (uint32_t)freqs[s] + cnt[wave][s] + rank[r];
+        const int top = xp ? 31 - __builtin_clz(xp) : log2L;
+        const int nb = top < log2L ? log2L - top : 0;
         const uint32_t base = xp << nb;
+        const uint32_t ex = (nsym == 256) ? (((s >> 4) << 11) | ((s & 0xFu) << 19)) : (s << 11);
         table[slot] = v2u{(uint32_t)nb | ex, (base - L) * 8u};
     }
 }
@@ -565,135 +606,185 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
 }
 
 // ---------------------------------------------------------------------
-// Standalone decode: G groups of one tensor per wave; output [N, K]
-// (element-major), one byte per lane and element.
+// Standalone decode: two adjacent groups of one tensor per wave (two
+// independent chains per lane); output [N, K], element-major.
+//
+// A tile leaves each lane with 16 bytes of its own column (rows 16t ..
+// 16t + 15).  A 4x4 byte transpose inside each quad of lanes (two DPP swaps
+// and two v_perm per word) turns every word into 4 columns of one row, so a
+// dword store per word writes 4 rows x 64 bytes and the wave's two groups
+// fill each 128-byte line of a row between them.  In a wave whose groups
+// are not both complete (the tensor's last lanes) each store is checked
+// against the lanes in range, down to single bytes.
 // ---------------------------------------------------------------------
-template <int SPS, int G>
+constexpr int kDecodeGroups = 2;
+
+// Word d of lane i in a quad holds rows 4j..4j+3 of column i; the result
+// holds columns 0..3 of row 4j+i.  sel1/sel2 are the lane's v_perm
+// selectors (quad_selectors).
+__device__ __forceinline__ uint32_t quad_transpose(uint32_t d, uint32_t sel1, uint32_t sel2) {
+    // DPP quad_perm [2,3,0,1]: the word of lane i^2; [1,0,3,2]: of lane i^1
+    const uint32_t x = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d, 0x4E, 0xF, 0xF, false);
+    d = __builtin_amdgcn_perm(x, d, sel1);
+    const uint32_t y = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d, 0xB1, 0xF, 0xF, false);
+    return __builtin_amdgcn_perm(y, d, sel2);
+}
+
+// Step 1 keeps the lane's own half and takes the partner's (lanes 0,1:
+// low halves; lanes 2,3: high halves); step 2 interleaves bytes the same way.
+__device__ __forceinline__ void quad_selectors(int lane, uint32_t& sel1, uint32_t& sel2) {
+    sel1 = (lane & 2) ? 0x03020706u : 0x05040100u;
+    sel2 = (lane & 1) ? 0x03070105u : 0x06020400u;
+}
+
+template <int SPS>
 struct DecodeWave {
-    Chains<G> ch;
-    v2u sm[G][2];
-    const char* pf[G];
-    uint32_t sm_bytes[G];
-    uint8_t* out[G];        // column k0 of row 0
-    bool active[G];
+    static constexpr int C = kDecodeGroups;
+    Chains<C> ch;
+    v2u sm[C][kSmAhead];    // sign/mantissa words of tiles t .. t + kSmAhead - 1 (by t mod kSmAhead)
+    const char* pf[C];      // sign/mantissa row of the next prefetch (wave-uniform)
+    uint32_t sm_bytes[C];   // bytes of a group's sm row (8 per lane in range)
+    int lanes[C];           // lanes of each group in range
+    uint8_t* out_tile;      // row 16t, column k0 (wave-uniform)
     const v2u* tbl;
     uint32_t* progress;
     uint32_t live;
-    int64_t K, N, sm_stride;
+    int64_t K;
+    int64_t sm_stride;      // K * 8
+    uint32_t qoff;          // (lane & 3) * K + (lane >> 2) * 4: the lane's word after the transpose
+    uint32_t sel1, sel2;
     int n_tiles;
     int lane;
+    bool full;              // both groups have 64 lanes in range (wave-uniform)
 
+    // Tile t (P = t mod kSmAhead) holding n elements per lane (n < 16 only
+    // for a ragged last tile).
     template <int P>
-    __device__ __forceinline__ void tile(int t) {
-        const int64_t e0 = (int64_t)t * kTile;
-        const int n = (int)(N - e0 < kTile ? N - e0 : kTile);
-        uint32_t ex[G][4];
-        if (n == kTile) {
-            dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, G>(ch, tbl, lane, ex);
-        } else {
-            dec_ragged<P>(n, ex);
-        }
+    __device__ __forceinline__ void tile(int t, int n) {
+        // A ragged tile is decoded in full: the steps past the lane's last
+        // symbol come after every real one, read zero or stale stream words
+        // and stay inside the table and the ring, and their bytes are not
+        // stored.
+        uint32_t ex[C][4];
+        dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, C>(ch, tbl, lane, ex);
         pace(progress, lane, (uint32_t)t, live);
+        uint32_t w[C][4];
         #pragma unroll
-        for (int g = 0; g < G; g++) {
-            uint32_t w[4];
-            compose8(ex[g][0], ex[g][1], sm[g][P].x, w[0], w[1]);
-            compose8(ex[g][2], ex[g][3], sm[g][P].y, w[2], w[3]);
-            if (active[g]) {
-                uint8_t* o = out[g] + e0 * K + lane;
+        for (int g = 0; g < C; g++) {
+            compose8(ex[g][0], ex[g][1], sm[g][P].x, w[g][0], w[g][1]);
+            compose8(ex[g][2], ex[g][3], sm[g][P].y, w[g][2], w[g][3]);
+        }
+        if (full && n == kTile) {   // wave-uniform
+            #pragma unroll
+            for (int g = 0; g < C; g++) {
                 #pragma unroll
-                for (int i = 0; i < kTile; i++)
-                    if (i < n) o[i * K] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+                for (int j = 0; j < 4; j++)
+                    *reinterpret_cast<uint32_t*>(out_tile + (int64_t)j * 4 * K + g * kLanes + qoff) =
+                        quad_transpose(w[g][j], sel1, sel2);
+            }
+        } else {
+            const int row_in_quad = lane & 3;
+            #pragma unroll
+            for (int g = 0; g < C; g++) {
+                // columns of this lane's transposed words that are in range
+                const int valid = lanes[g] - 4 * (lane >> 2);
+                #pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t v = quad_transpose(w[g][j], sel1, sel2);
+                    uint8_t* p = out_tile + (int64_t)j * 4 * K + g * kLanes + qoff;
+                    if (4 * j + row_in_quad < n && valid > 0) {
+                        if (valid >= 4) {
+                            *reinterpret_cast<uint32_t*>(p) = v;
+                        } else {
+                            p[0] = (uint8_t)v;
+                            if (valid > 1) p[1] = (uint8_t)(v >> 8);
+                            if (valid > 2) p[2] = (uint8_t)(v >> 16);
+                        }
+                    }
+                }
             }
         }
+        out_tile += kTile * K;
+        // sign/mantissa of tile min(t + kSmAhead, n_tiles - 1): the loads are unconditional
         #pragma unroll
-        for (int g = 0; g < G; g++)
+        for (int g = 0; g < C; g++)
             sm[g][P] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(pf[g], sm_bytes[g]),
                                                             (uint32_t)lane * 8u, 0, kNT);
-        if (t + 3 < n_tiles) {
+        if (t + kSmAhead + 1 < n_tiles) {
             #pragma unroll
-            for (int g = 0; g < G; g++) pf[g] += sm_stride;
+            for (int g = 0; g < C; g++) pf[g] += sm_stride;
         }
     }
 
-    // Last tile with fewer than 16 elements: the same stages, fewer steps.
-    template <int P>
-    __device__ __forceinline__ void dec_ragged(int n, uint32_t (&ex)[G][4]) {
-        constexpr int ST0 = (P * Alpha<SPS>::kStagesPerTile) % kDelay;
-        const int steps = n / SPS;
-        #pragma unroll
-        for (int g = 0; g < G; g++) ex[g][0] = ex[g][1] = ex[g][2] = ex[g][3] = 0;
-        static_for<0, Alpha<SPS>::kStagesPerTile>([&](auto H) {
-            constexpr int h = decltype(H)::value;
-            #pragma unroll
-            for (int g = 0; g < G; g++) feed_stage<(ST0 + h) % kDelay>(ch.f[g], ch.p[g], lane);
-            for (int q = 0; q < 2 * kChecksPerStage; q++) {
-                const int i = h * 2 * kChecksPerStage + q;
-                if (i >= steps) break;
-                #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    if ((q & 1) == 0) refill(ch.l[g], ch.f[g]);
-                    const uint32_t e = dec_step(ch.l[g], tbl);
-                    if constexpr (SPS == 2) ex[g][i >> 1] |= ((e >> 8) & 0xFFFFu) << (16 * (i & 1));
-                    else ex[g][i >> 2] |= ((e >> 8) & 0xFFu) << (8 * (i & 3));
-                }
-            }
-        });
+    // All tiles, four per iteration (the sign/mantissa buffers rotate by
+    // four); the last tile holds n_last elements.
+    __device__ __forceinline__ void run(int n_last) {
+        static_assert(kSmAhead == 4, "the loop below is unrolled for kSmAhead == 4");
+        for (int t = 0; t < n_tiles; t += kSmAhead) {
+            tile<0>(t, t + 1 < n_tiles ? kTile : n_last);
+            if (t + 1 < n_tiles) tile<1>(t + 1, t + 2 < n_tiles ? kTile : n_last);
+            if (t + 2 < n_tiles) tile<2>(t + 2, t + 3 < n_tiles ? kTile : n_last);
+            if (t + 3 < n_tiles) tile<3>(t + 3, t + 4 < n_tiles ? kTile : n_last);
+        }
     }
 };
 
-template <int SPS, int G>
+template <int SPS>
 __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     const uint32_t* __restrict__ comp, int64_t words, const int64_t* __restrict__ off,
     const uint16_t* __restrict__ st, const v2u* __restrict__ sm,
     const v2u* __restrict__ table, int64_t K, int64_t N, uint8_t* __restrict__ out) {
     constexpr uint32_t L = Alpha<SPS>::L;
-    __shared__ DecSmem<SPS, G> smem;
+    constexpr int C = kDecodeGroups;
+    __shared__ DecSmem<SPS, C> smem;
     v2u* tbl = smem.tbl;
     load_table<L>(tbl, table);
     if (threadIdx.x == 0) smem.progress = 0;
     __syncthreads();
     const int lane = threadIdx.x & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
-    const int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
-    if (g0 * kLanes >= K) return;
+    const int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * C;
+    if (g0 * kLanes >= K) return;   // wave-uniform
     const int64_t n_groups = (K + kLanes - 1) / kLanes;
-    const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * G;
-    DecodeWave<SPS, G> w;
+    const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * C;
+    DecodeWave<SPS> w;
     w.progress = &smem.progress;
-    w.live = (uint32_t)(wg_groups >= (int64_t)kDecWaves * G ? kDecWaves : (wg_groups + G - 1) / G);
+    w.live = (uint32_t)(wg_groups >= (int64_t)kDecWaves * C ? kDecWaves : (wg_groups + C - 1) / C);
     w.lane = lane;
     w.K = K;
-    w.N = N;
-    w.n_tiles = (int)((N + kTile - 1) / kTile);
+    const int rag = (int)(N % kTile);
+    w.n_tiles = (int)(N / kTile) + (rag ? 1 : 0);
     w.tbl = tbl;
     w.sm_stride = K * 8;
-    const int64_t t1 = w.n_tiles > 1 ? 1 : 0;
-    const int64_t t2 = w.n_tiles > 2 ? 2 : w.n_tiles - 1;
+    w.out_tile = out + g0 * kLanes;
+    w.qoff = (uint32_t)(lane & 3) * (uint32_t)K + (uint32_t)(lane >> 2) * 4u;
+    quad_selectors(lane, w.sel1, w.sel2);
+    bool full = true;
     #pragma unroll
-    for (int j = 0; j < G; j++) {
+    for (int j = 0; j < C; j++) {
+        // a wave past the last group repeats it with no lanes in range
         const int64_t g = g0 + j < n_groups ? g0 + j : n_groups - 1;
         const int64_t k0 = g * kLanes;
         const int lanes = g0 + j < n_groups ? (K - k0 < kLanes ? (int)(K - k0) : kLanes) : 0;
-        w.active[j] = lane < lanes;
-        const uint32_t lane_ld = (uint32_t)(w.active[j] ? lane : (lanes ? lanes - 1 : 0));
+        full = full && lanes == kLanes;
+        w.lanes[j] = lanes;
+        const bool active = lane < lanes;
+        const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
         w.sm_bytes[j] = (uint32_t)lanes * 8u;
-        w.out[j] = out + k0;
         feed_init(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], lane, w.ch.p[j]);
-        lane_init(w.ch.l[j], w.active[j], st[k0 + lane_ld], L);
+        lane_init(w.ch.l[j], active, st[k0 + lane_ld], L);
         const char* row = reinterpret_cast<const char*>(sm + k0);
-        w.sm[j][0] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(row, w.sm_bytes[j]),
-                                                          (uint32_t)lane * 8u, 0, kNT);
-        w.sm[j][1] = __builtin_amdgcn_raw_buffer_load_b64(
-            rsrc(row + t1 * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
-        w.pf[j] = row + t2 * w.sm_stride;
+        #pragma unroll
+        for (int i = 0; i < kSmAhead; i++) {
+            const int64_t ti = i < w.n_tiles ? i : w.n_tiles - 1;
+            w.sm[j][i] = __builtin_amdgcn_raw_buffer_load_b64(
+                rsrc(row + ti * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+        }
+        const int64_t tn = kSmAhead < w.n_tiles ? kSmAhead : w.n_tiles - 1;
+        w.pf[j] = row + tn * w.sm_stride;
     }
-    int t = 0;
-    for (; t + 2 <= w.n_tiles; t += 2) {
-        w.template tile<0>(t);
-        w.template tile<1>(t + 1);
-    }
-    if (t < w.n_tiles) w.template tile<0>(t);
+    w.full = full;
+    w.run(rag ? rag : kTile);
 }
 
 int fail(int code, const std::string& msg) {
@@ -712,7 +803,6 @@ int sps_for(int32_t log2L) {
 
 template <int SPS>
 constexpr int kFusedGroups = 1;   // groups per wave in the fused kernel
-constexpr int kDecodeGroups = 2;   // groups per wave in the standalone decoder
 
 }  // namespace
 
@@ -743,7 +833,7 @@ int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs, 
     if (!spread || !freqs || !table) return fail(TANS_EINVAL, "table: null pointer");
     if (!((nsym == 256 && log2L == TANS_PAIR_LOG2L) || (nsym == 16 && log2L == TANS_NIBBLE_LOG2L)))
         return fail(TANS_EINVAL, "table: need (nsym 256, log2L 12) or (nsym 16, log2L 11)");
-    hipLaunchKernelGGL(table_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, spread, freqs,
+    hipLaunchKernelGGL(table_kernel, dim3(1), dim3(kTableWaves * 64), 0, (hipStream_t)stream, spread, freqs,
                        (int)nsym, (int)log2L, (v2u*)table);
     return hip_check(hipGetLastError(), "table_kernel launch");
 }
@@ -792,12 +882,14 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
     if (comp_bytes < 0 || comp_bytes % 4)
         return fail(TANS_EINVAL, "decode: compressed size must be a multiple of 4 bytes");
     if ((N + kTile - 1) / kTile > INT32_MAX) return fail(TANS_EINVAL, "decode: N too large");
+    // the stores address 4 rows of a tile with 32-bit offsets
+    if (K > (int64_t(1) << 30)) return fail(TANS_EINVAL, "decode: more than 2^30 lanes");
     const int64_t groups = (K + kLanes - 1) / kLanes;
     const int64_t per_block = (int64_t)kDecWaves * kDecodeGroups;
     const int64_t blocks = (groups + per_block - 1) / per_block;
     if (blocks > INT32_MAX) return fail(TANS_EINVAL, "decode: K too large");
 #define TANS_LAUNCH_DECODE(S)                                                                     \
-    hipLaunchKernelGGL((decode_kernel<S, kDecodeGroups>), dim3((unsigned)blocks),                \
+    hipLaunchKernelGGL((decode_kernel<S>), dim3((unsigned)blocks),                               \
                        dim3(kDecBlock), 0, (hipStream_t)stream, (const uint32_t*)comp,           \
                        comp_bytes / 4, offsets, states, (const v2u*)sm, (const v2u*)table, K, N, \
                        (uint8_t*)out)

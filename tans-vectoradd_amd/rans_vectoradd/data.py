@@ -54,10 +54,16 @@ def gaussian_fp8_bytes(n: int, *, std: float = 0.02, seed: int = 0,
 
 def laplace_fp8_bytes(n: int, *, b: float = 0.015, seed: int = 0,
                       device: str | torch.device = "cpu") -> tuple[torch.Tensor, float]:
-    """n bytes of Laplace(0, b) (inverse CDF), scaled and cast as above."""
+    """n bytes of Laplace(0, b) (inverse CDF), scaled and cast as above.
+
+    torch.rand can return exactly 0, i.e. u = -0.5, where the inverse CDF
+    is infinite (about 64 times in 2^30 draws), and one infinity would
+    scale every other value to zero; 2|u| is therefore capped at 1 - 2^-24,
+    the largest float32 below 1, which bounds |x| by 24 ln2 b."""
     g = torch.Generator(device=device).manual_seed(seed)
     u = torch.rand(n, generator=g, device=device) - 0.5
-    x = -b * torch.sign(u) * torch.log1p(-2.0 * u.abs())
+    a = (2.0 * u.abs()).clamp_max_(1.0 - 2.0 ** -24)
+    x = -b * torch.sign(u) * torch.log1p(-a)
     return _scale_to_fp8(x)
 
 

@@ -78,9 +78,36 @@ def test_table_device_matches_host(R, alphabet):
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
+def test_table_device_any_spread(R, alphabet):
+    """Device table for a spread that is not the hash walk: the symbol
+    multiset of the frequencies in a random slot order."""
+    from rans_vectoradd import tans_codec as T
+    _say(f"case: device table, shuffled spread ({alphabet})")
+    nsym, L = (256, 4096) if alphabet == "pair" else (16, 2048)
+    rng = np.random.default_rng(11)
+    f = T.symbol_freqs(R.QWEN3_14B_FP8_EXP, alphabet)
+    sp = rng.permutation(np.repeat(np.arange(nsym, dtype=np.int32), f)).astype(np.int32)
+    host = T.build_decode_table(sp, f)
+    dev = torch.empty(2 * L, dtype=torch.int32, device="cuda")
+    from rans_vectoradd._lib import lib
+    stream = torch.cuda.current_stream().cuda_stream
+    sp_d = torch.from_numpy(sp).cuda()
+    f_d = torch.from_numpy(f).cuda()
+    assert lib.tans_build_decode_table_device(sp_d.data_ptr(), f_d.data_ptr(), nsym,
+                                              L.bit_length() - 1, dev.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(dev.cpu(), host)
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
 @pytest.mark.parametrize("K,N", [(128, 128), (1024, 128), (10000, 128), (100000, 128),
-                                 (64, 2), (65, 18), (200, 130), (3, 1000)])
+                                 (64, 2), (65, 18), (200, 130), (3, 1000),
+                                 (130, 30), (192, 64), (66, 80), (1, 16), (4096, 14)])
 def test_decode_roundtrip(R, alphabet, K, N):
+    """The reference's cases (test_gpu_decode_tans.py:69-74) plus ragged
+    ones: partial last groups of 1, 2, 3, 8, 16, 32 lanes, a wave holding one
+    complete group and no second one (K = 192), and last tiles of 2, 8, 14
+    elements."""
     from rans_vectoradd import tans_codec as T
     _say(f"case: gpu_tans_decode K={K} N={N} {alphabet}")
     exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
@@ -112,6 +139,25 @@ def test_vecadd_fused_vs_raw_and_oracle(R, lut, alphabet, K, N):
     ref = O.vecadd(lut, fa.numpy(), fb.numpy()).reshape(K, N)
     ok = (fused.numpy() == ref) | O.nan_mask_lut()[fa.numpy(), fb.numpy()]
     assert ok.all()
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("dist", ["gaussian", "laplace"])
+def test_decode_config2_data_2p24(R, alphabet, dist):
+    """Config-2 data (N(0, 0.02) and Laplace(0, 0.015), scaled to 448, the
+    data's own table) at 2^24 elements, 1024 per lane: bit-exact round trip."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: gpu_tans_decode {dist} 2^24 {alphabet}")
+    n, N = 1 << 24, 1024
+    K = n // N
+    gen = D.gaussian_fp8_bytes if dist == "gaussian" else D.laplace_fp8_bytes
+    q, _ = gen(n, seed=5)
+    hist = D.exp_histogram(q)
+    assert (hist > 0).sum() >= 12           # a real spread of exponents
+    e = T.encode(q.reshape(K, N), hist, alphabet=alphabet)
+    comp, st, off, part, sm, fr, sp = [x.cuda() for x in e]
+    dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
+    assert torch.equal(dec.cpu(), q.reshape(K, N).t())
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
