@@ -136,6 +136,32 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
                 const uint32_t* table, int32_t log2L,
                 int64_t K, int64_t N, void* out, void* stream);
 
+/* ---------------- Fused decode + skinny GEMM (no counterpart in the
+ * reference: its rows a15 / configs 3-4 are new) ----------------------- */
+
+/* y[b][r] = bf16(scale * sum_c W[r][c] * x[b][c]), fp32 accumulation,
+ * round-to-nearest-even to bf16; W is R x C FP8 E4M3FN, tANS-coded as
+ * written by rans_vectoradd.tans_codec.encode_matrix: rows padded to
+ * Rp = R rounded up to 64, columns cut into S segments of Nc (even,
+ * <= 512) columns with (S - 1) * Nc < C <= S * Nc, lane s * Rp + r holding
+ * row r of segment s; comp/offsets/states/sm are that encoding (K = S * Rp
+ * lanes of Nc elements) and table its decode table.
+ *   x          bf16 [B, C], 1 <= B <= 8
+ *   workspace  device memory of at least S * B * Rp * 4 bytes (per-segment
+ *              fp32 partial sums; contents on entry do not matter)
+ *   y          bf16 [B, R]
+ * Partial sums are added in segment order, so results are deterministic. */
+int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* offsets,
+                        const uint16_t* states, const void* sm, const uint32_t* table,
+                        int32_t log2L, int64_t R, int64_t C, int64_t S, int64_t Nc,
+                        const void* x, int64_t B, float scale, void* workspace,
+                        int64_t workspace_bytes, void* y, void* stream);
+
+/* The same product from uncompressed FP8 W [R, C] (row-major), C % 16 == 0:
+ * the baseline the fused kernel is measured against.                    */
+int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_t B,
+                      float scale, void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

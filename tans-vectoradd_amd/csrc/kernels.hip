@@ -787,6 +787,266 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     w.run(rag ? rag : kTile);
 }
 
+// ---------------------------------------------------------------------
+// Fused decode + skinny GEMM: y[b][r] = scale * sum_c W[r][c] * x[b][c]
+// with W tANS-coded and B <= 8 rows of bf16 x.
+//
+// Encoding (rans_vectoradd.tans_codec.encode_matrix): W, padded to Rp rows
+// (a multiple of 64) and S * Nc columns, is cut into S column segments of
+// Nc columns; lane s * Rp + r holds row r of segment s, so a group is 64
+// rows of one segment and every lane of a wave works on the same columns.
+//
+// A workgroup takes one segment and up to 32 row groups (two per wave, two
+// chains per lane).  It stages the segment's x columns in LDS (zero past
+// the matrix and past the segment), and each tile's 16 FP8 weights per
+// lane become 8 bf16 pairs (exact) that meet x in v_dot2_f32_bf16 with
+// fp32 accumulation; x is read once per tile and batch row with a
+// wave-uniform LDS address (a broadcast).  Partial sums go to a workspace
+// [S][B][Rp] and gemm_finalize_kernel adds the S segments in order, scales
+// and rounds to bf16 (round to nearest even).
+// ---------------------------------------------------------------------
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+constexpr int kGemmChains = 2;                        // row groups per wave
+constexpr int kGemmGroupsPerBlock = kDecWaves * kGemmChains;
+constexpr int kGemmMaxBatch = 8;
+constexpr int kGemmMaxSegCols = 512;                  // Nc limit: the x stage is 8 KiB
+
+template <int SPS>
+struct GemmSmem {
+    DecSmem<SPS, kGemmChains> dec;
+    uint32_t xs[kGemmMaxBatch * kGemmMaxSegCols / 2];  // bf16 pairs [B][Nc16 / 2]
+};
+
+template <int SPS, int NB>
+struct GemmWave {
+    static constexpr int C = kGemmChains;
+    Chains<C> ch;
+    v2u sm[C][kSmAhead];
+    const char* pf[C];
+    uint32_t sm_bytes;
+    const v2u* tbl;
+    const uint32_t* xs;     // LDS x stage of the segment
+    uint32_t x_row;         // dwords per batch row in the stage
+    uint32_t* progress;
+    uint32_t live;
+    int64_t sm_stride;
+    int n_tiles;
+    int lane;
+    float acc[C][NB];
+
+    template <int P>
+    __device__ __forceinline__ void tile(int t, int n) {
+        // a ragged last tile is decoded in full (see DecodeWave::tile) and
+        // its bytes past n are zeroed before they are used
+        uint32_t ex[C][4];
+        dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, C>(ch, tbl, lane, ex);
+        pace(progress, lane, (uint32_t)t, live);
+        v2bf wb[C][8];   // bf16 pairs: elements (2m, 2m + 1) of the tile
+        #pragma unroll
+        for (int c = 0; c < C; c++) {
+            uint32_t w[4];
+            compose8(ex[c][0], ex[c][1], sm[c][P].x, w[0], w[1]);
+            compose8(ex[c][2], ex[c][3], sm[c][P].y, w[2], w[3]);
+            #pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (n < kTile) {   // wave-uniform
+                    const int keep = n - 4 * j;
+                    w[j] = keep >= 4 ? w[j] : (keep <= 0 ? 0u : w[j] & ((1u << (8 * keep)) - 1u));
+                }
+                wb[c][2 * j] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[j], 1.0f, false);
+                wb[c][2 * j + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[j], 1.0f, true);
+            }
+        }
+        #pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const v4u* xp = reinterpret_cast<const v4u*>(xs + b * x_row + t * 8);
+            const v4u x0 = xp[0];
+            const v4u x1 = xp[1];
+            const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            #pragma unroll
+            for (int c = 0; c < C; c++) {
+                float a = acc[c][b];
+                #pragma unroll
+                for (int m = 0; m < 8; m++)
+                    a = __builtin_amdgcn_fdot2_f32_bf16(wb[c][m], __builtin_bit_cast(v2bf, xv[m]),
+                                                        a, false);
+                acc[c][b] = a;
+            }
+        }
+        #pragma unroll
+        for (int c = 0; c < C; c++)
+            sm[c][P] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(pf[c], sm_bytes),
+                                                            (uint32_t)lane * 8u, 0, kNT);
+        if (t + kSmAhead + 1 < n_tiles) {
+            #pragma unroll
+            for (int c = 0; c < C; c++) pf[c] += sm_stride;
+        }
+    }
+
+    __device__ __forceinline__ void run(int n_last) {
+        static_assert(kSmAhead == 4, "the loop below is unrolled for kSmAhead == 4");
+        for (int t = 0; t < n_tiles; t += kSmAhead) {
+            tile<0>(t, t + 1 < n_tiles ? kTile : n_last);
+            if (t + 1 < n_tiles) tile<1>(t + 1, t + 2 < n_tiles ? kTile : n_last);
+            if (t + 2 < n_tiles) tile<2>(t + 2, t + 3 < n_tiles ? kTile : n_last);
+            if (t + 3 < n_tiles) tile<3>(t + 3, t + 4 < n_tiles ? kTile : n_last);
+        }
+    }
+};
+
+// Grid: S * row_blocks workgroups; block (s, rb) decodes row groups
+// [32 rb, 32 rb + 32) of segment s.  R: rows, Rp: rows padded to 64,
+// C: columns, Nc: columns per segment.
+template <int SPS, int NB>
+__global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
+    const uint32_t* __restrict__ comp, int64_t words, const int64_t* __restrict__ off,
+    const uint16_t* __restrict__ st, const v2u* __restrict__ sm, const v2u* __restrict__ table,
+    int64_t Rp, int64_t C, int S, int Nc, int row_blocks, const uint16_t* __restrict__ x,
+    float* __restrict__ ws) {
+    constexpr uint32_t L = Alpha<SPS>::L;
+    constexpr int CH = kGemmChains;
+    __shared__ GemmSmem<SPS> smem;
+    const int s = (int)(blockIdx.x / (unsigned)row_blocks);
+    const int rb = (int)(blockIdx.x % (unsigned)row_blocks);
+    const int64_t n_rg = Rp / kLanes;                       // row groups per segment
+    // stage x[b][s * Nc + c] for c < Nc16 (zero past the segment or the matrix)
+    const int nc16 = (Nc + kTile - 1) / kTile * kTile;
+    const uint32_t x_row = (uint32_t)nc16 / 2;
+    uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem.xs);
+    for (int i = threadIdx.x; i < NB * nc16; i += blockDim.x) {
+        const int b = i / nc16, c = i % nc16;
+        const int64_t col = (int64_t)s * Nc + c;
+        xs16[i] = (c < Nc && col < C) ? x[(int64_t)b * C + col] : (uint16_t)0;
+    }
+    v2u* tbl = smem.dec.tbl;
+    load_table<L>(tbl, table);
+    if (threadIdx.x == 0) smem.dec.progress = 0;
+    __syncthreads();
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
+    const int64_t rg0 = (int64_t)rb * kGemmGroupsPerBlock + (int64_t)wave * CH;
+    if (rg0 >= n_rg) return;   // wave-uniform
+    const int64_t rg_left = n_rg - (int64_t)rb * kGemmGroupsPerBlock;
+    GemmWave<SPS, NB> w;
+    w.progress = &smem.dec.progress;
+    w.live = (uint32_t)(rg_left >= kGemmGroupsPerBlock ? kDecWaves : (rg_left + CH - 1) / CH);
+    w.lane = lane;
+    w.tbl = tbl;
+    w.xs = smem.xs;
+    w.x_row = x_row;
+    w.sm_stride = (int64_t)S * Rp * 8;                      // lanes: S * Rp
+    const int rag = Nc % kTile;
+    w.n_tiles = Nc / kTile + (rag ? 1 : 0);
+    w.sm_bytes = kLanes * 8u;
+    #pragma unroll
+    for (int j = 0; j < CH; j++) {
+        // a wave with one row group left repeats it as its second chain and
+        // discards that chain's sums
+        const int64_t rg = rg0 + j < n_rg ? rg0 + j : n_rg - 1;
+        const int64_t g = (int64_t)s * n_rg + rg;
+        const int64_t k0 = g * kLanes;
+        feed_init(w.ch.f[j], comp, words, off, g, smem.dec.rings[wave][j], lane, w.ch.p[j]);
+        lane_init(w.ch.l[j], true, st[k0 + lane], L);
+        const char* row = reinterpret_cast<const char*>(sm + k0);
+        #pragma unroll
+        for (int i = 0; i < kSmAhead; i++) {
+            const int64_t ti = i < w.n_tiles ? i : w.n_tiles - 1;
+            w.sm[j][i] = __builtin_amdgcn_raw_buffer_load_b64(
+                rsrc(row + ti * w.sm_stride, w.sm_bytes), (uint32_t)lane * 8u, 0, kNT);
+        }
+        const int64_t tn = kSmAhead < w.n_tiles ? kSmAhead : w.n_tiles - 1;
+        w.pf[j] = row + tn * w.sm_stride;
+        #pragma unroll
+        for (int b = 0; b < NB; b++) w.acc[j][b] = 0.0f;
+    }
+    w.run(rag ? rag : kTile);
+    #pragma unroll
+    for (int j = 0; j < CH; j++) {
+        if (rg0 + j >= n_rg) break;
+        const int64_t r = (rg0 + j) * kLanes + lane;
+        #pragma unroll
+        for (int b = 0; b < NB; b++) ws[((int64_t)s * NB + b) * Rp + r] = w.acc[j][b];
+    }
+}
+
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);   // quiet NaN
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// y[b][r] = bf16(scale * sum over s of ws[s][b][r]), s in ascending order.
+__global__ __launch_bounds__(256) void gemm_finalize_kernel(const float* __restrict__ ws, int S,
+                                                            int NB, int64_t Rp, int64_t R,
+                                                            float scale, uint16_t* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)NB * R) return;
+    const int64_t b = i / R, r = i % R;
+    float a = 0.0f;
+    for (int s = 0; s < S; s++) a += ws[((int64_t)s * NB + b) * Rp + r];
+    y[i] = bf16_rne(a * scale);
+}
+
+// Uncompressed FP8 skinny GEMM (the baseline of the fused one): a wave
+// takes 4 rows; each lane walks 16-column blocks, converting W to bf16
+// pairs and accumulating v_dot2_f32_bf16 against x read from global memory
+// (cache-resident), then the wave sums its lanes.  C % 16 == 0.
+constexpr int kRawRows = 4;
+
+__device__ __forceinline__ float wave_sum(float v) {
+    #pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+template <int NB>
+__global__ __launch_bounds__(256) void gemm_raw_kernel(const v4u* __restrict__ W, int64_t R,
+                                                       int64_t C, const v4u* __restrict__ x,
+                                                       float scale, uint16_t* __restrict__ y) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t r0 = ((int64_t)blockIdx.x * (256 / kLanes) + threadIdx.x / kLanes) * kRawRows;
+    if (r0 >= R) return;
+    const int64_t cb = C / 16;                 // 16-column blocks per row
+    float acc[kRawRows][NB];
+    #pragma unroll
+    for (int i = 0; i < kRawRows; i++)
+        #pragma unroll
+        for (int b = 0; b < NB; b++) acc[i][b] = 0.0f;
+    for (int64_t k = lane; k < cb; k += kLanes) {
+        v2bf wb[kRawRows][8];
+        #pragma unroll
+        for (int i = 0; i < kRawRows; i++) {
+            const int64_t r = r0 + i < R ? r0 + i : R - 1;
+            const v4u v = __builtin_nontemporal_load(W + r * cb + k);
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+            #pragma unroll
+            for (int j = 0; j < 4; j++) {
+                wb[i][2 * j] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wv[j], 1.0f, false);
+                wb[i][2 * j + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wv[j], 1.0f, true);
+            }
+        }
+        #pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const v4u x0 = x[(b * C) / 8 + 2 * k];
+            const v4u x1 = x[(b * C) / 8 + 2 * k + 1];
+            const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            #pragma unroll
+            for (int i = 0; i < kRawRows; i++)
+                #pragma unroll
+                for (int m = 0; m < 8; m++)
+                    acc[i][b] = __builtin_amdgcn_fdot2_f32_bf16(
+                        wb[i][m], __builtin_bit_cast(v2bf, xv[m]), acc[i][b], false);
+        }
+    }
+    #pragma unroll
+    for (int i = 0; i < kRawRows; i++)
+        #pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float v = wave_sum(acc[i][b]);
+            if (lane == 0 && r0 + i < R) y[b * R + r0 + i] = bf16_rne(v * scale);
+        }
+}
+
 int fail(int code, const std::string& msg) {
     tans_internal_set_error(msg.c_str());
     return code;
@@ -897,6 +1157,75 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
     else TANS_LAUNCH_DECODE(1);
 #undef TANS_LAUNCH_DECODE
     return hip_check(hipGetLastError(), "decode_kernel launch");
+}
+
+int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* offsets,
+                        const uint16_t* states, const void* sm, const uint32_t* table,
+                        int32_t log2L, int64_t R, int64_t C, int64_t S, int64_t Nc, const void* x,
+                        int64_t B, float scale, void* workspace, int64_t workspace_bytes, void* y,
+                        void* stream) {
+    const int sps = sps_for(log2L);
+    if (!sps) return fail(TANS_EINVAL, "gemm_fused: log2L must be 12 (pair) or 11 (nibble)");
+    if (R <= 0 || C <= 0 || S <= 0 || Nc <= 0 || Nc % 2)
+        return fail(TANS_EINVAL, "gemm_fused: need R, C, S > 0 and an even segment width");
+    if (Nc > kGemmMaxSegCols) return fail(TANS_EINVAL, "gemm_fused: segment width above 512");
+    if (S * Nc < C || (S - 1) * Nc >= C)
+        return fail(TANS_EINVAL, "gemm_fused: S segments of Nc columns must cover C exactly");
+    if (B < 1 || B > kGemmMaxBatch) return fail(TANS_EINVAL, "gemm_fused: batch must be 1..8");
+    if (!comp || !offsets || !states || !sm || !table || !x || !workspace || !y)
+        return fail(TANS_EINVAL, "gemm_fused: null pointer");
+    if (comp_bytes < 0 || comp_bytes % 4)
+        return fail(TANS_EINVAL, "gemm_fused: compressed size must be a multiple of 4 bytes");
+    const int64_t Rp = (R + kLanes - 1) / kLanes * kLanes;
+    if (workspace_bytes < S * B * Rp * 4)
+        return fail(TANS_EINVAL, "gemm_fused: workspace smaller than S * B * Rp * 4 bytes");
+    const int64_t row_blocks = (Rp / kLanes + kGemmGroupsPerBlock - 1) / kGemmGroupsPerBlock;
+    const int64_t blocks = S * row_blocks;
+    if (blocks > INT32_MAX || B * R / 256 + 1 > INT32_MAX)
+        return fail(TANS_EINVAL, "gemm_fused: matrix too large");
+    hipStream_t st = (hipStream_t)stream;
+#define TANS_GEMM_CASE(S_, NB)                                                                    \
+    case NB:                                                                                      \
+        hipLaunchKernelGGL((gemm_fused_kernel<S_, NB>), dim3((unsigned)blocks), dim3(kDecBlock), 0, \
+                           st, (const uint32_t*)comp, comp_bytes / 4, offsets, states,            \
+                           (const v2u*)sm, (const v2u*)table, Rp, C, (int)S, (int)Nc,             \
+                           (int)row_blocks, (const uint16_t*)x, (float*)workspace);               \
+        break;
+#define TANS_GEMM_SWITCH(S_)                                                                      \
+    switch ((int)B) {                                                                             \
+        TANS_GEMM_CASE(S_, 1) TANS_GEMM_CASE(S_, 2) TANS_GEMM_CASE(S_, 3) TANS_GEMM_CASE(S_, 4)   \
+        TANS_GEMM_CASE(S_, 5) TANS_GEMM_CASE(S_, 6) TANS_GEMM_CASE(S_, 7) TANS_GEMM_CASE(S_, 8)   \
+    }
+    if (sps == 2) { TANS_GEMM_SWITCH(2) } else { TANS_GEMM_SWITCH(1) }
+#undef TANS_GEMM_SWITCH
+#undef TANS_GEMM_CASE
+    int rc = hip_check(hipGetLastError(), "gemm_fused_kernel launch");
+    if (rc != TANS_OK) return rc;
+    hipLaunchKernelGGL(gemm_finalize_kernel, dim3((unsigned)((B * R + 255) / 256)), dim3(256), 0,
+                       st, (const float*)workspace, (int)S, (int)B, Rp, R, scale, (uint16_t*)y);
+    return hip_check(hipGetLastError(), "gemm_finalize_kernel launch");
+}
+
+int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_t B, float scale,
+                      void* y, void* stream) {
+    if (R <= 0 || C <= 0 || C % 16) return fail(TANS_EINVAL, "gemm_raw: need R > 0 and C a positive multiple of 16");
+    if (B < 1 || B > kGemmMaxBatch) return fail(TANS_EINVAL, "gemm_raw: batch must be 1..8");
+    if (!w || !x || !y) return fail(TANS_EINVAL, "gemm_raw: null pointer");
+    const int64_t rows_per_block = (256 / kLanes) * kRawRows;
+    const int64_t blocks = (R + rows_per_block - 1) / rows_per_block;
+    if (blocks > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
+    hipStream_t st = (hipStream_t)stream;
+#define TANS_RAW_CASE(NB)                                                                         \
+    case NB:                                                                                      \
+        hipLaunchKernelGGL((gemm_raw_kernel<NB>), dim3((unsigned)blocks), dim3(256), 0, st,       \
+                           (const v4u*)w, R, C, (const v4u*)x, scale, (uint16_t*)y);              \
+        break;
+    switch ((int)B) {
+        TANS_RAW_CASE(1) TANS_RAW_CASE(2) TANS_RAW_CASE(3) TANS_RAW_CASE(4)
+        TANS_RAW_CASE(5) TANS_RAW_CASE(6) TANS_RAW_CASE(7) TANS_RAW_CASE(8)
+    }
+#undef TANS_RAW_CASE
+    return hip_check(hipGetLastError(), "gemm_raw_kernel launch");
 }
 
 }  // extern "C"

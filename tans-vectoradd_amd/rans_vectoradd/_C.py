@@ -22,8 +22,8 @@ import ctypes
 
 import torch
 
-from ._lib import (TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PAIR_LOG2L, TANS_TILE, check,
-                   lib)
+from ._lib import (TANS_GEMM_MAX_BATCH, TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PAIR_LOG2L,
+                   TANS_TILE, check, lib)
 
 __all__ = [
     "tans_encode_interleaved",
@@ -31,6 +31,8 @@ __all__ = [
     "fp8_memcpy",
     "fp8_vecadd_raw",
     "fp8_vecadd_fused_tans",
+    "fp8_gemm_fused_tans",
+    "fp8_gemm_raw",
 ]
 
 
@@ -215,3 +217,62 @@ def fp8_vecadd_fused_tans(a_comp: torch.Tensor, a_offsets: torch.Tensor, a_state
                                         _ptr(decode_tbl), log2L, K, N, _ptr(out), _stream(dev)),
               "fp8_vecadd_fused_tans")
     return out
+
+
+def _batch_view(x: torch.Tensor, C: int):
+    """x bf16 [C] or [B, C] -> (x2d [B, C], B, squeeze)."""
+    _check_dev("x", x, torch.bfloat16)
+    _require(x.dim() in (1, 2) and x.shape[-1] == C, f"x must be [C] or [B, C] with C = {C}")
+    x2 = x.view(1, C) if x.dim() == 1 else x
+    B = x2.shape[0]
+    _require(1 <= B <= TANS_GEMM_MAX_BATCH, f"batch must be 1..{TANS_GEMM_MAX_BATCH}")
+    return x2, B, x.dim() == 1
+
+
+def fp8_gemm_fused_tans(m, decode_tbl: torch.Tensor, x: torch.Tensor,
+                        scale: float = 1.0) -> torch.Tensor:
+    """y = scale * (W @ x^T) as bf16, W decoded from its tANS encoding inside
+    the kernel.  No counterpart in the reference (its configs 3-4).
+
+    m: a TansMatrix from tans_codec.encode_matrix, its tensors on the GPU;
+    decode_tbl: build_decode_table of its spread/freqs (on the GPU);
+    x: bf16 [C] or [B, C] (B <= 8).  Returns bf16 [R] or [B, R]; fp32
+    accumulation, segment sums added in a fixed order."""
+    R, C, S, Nc = m.rows, m.cols, m.segments, m.seg_cols
+    for name in ("comp", "sm"):
+        _check_dev(name, getattr(m, name), torch.uint8)
+    _check_dev("offsets", m.offsets, torch.int64)
+    _check_dev("states", m.states, torch.uint16)
+    _check_dev("decode_tbl", decode_tbl, torch.int32)
+    x2, B, squeeze = _batch_view(x, C)
+    Rp = (R + TANS_LANES - 1) // TANS_LANES * TANS_LANES
+    K = S * Rp
+    _require(m.states.numel() == K, "states do not match the matrix shape")
+    _require(m.offsets.numel() == _groups(K) + 1, "offsets do not match the matrix shape")
+    _require(m.sm.numel() == _sm_bytes(K, Nc), "sign/mantissa tiles do not match the matrix shape")
+    log2L = log2_states(decode_tbl.numel() // 2)
+    dev = m.comp.device
+    for t in (m.offsets, m.states, m.sm, decode_tbl, x2):
+        _require(t.device == dev, "all tensors must be on one device")
+    y = torch.empty((B, R), dtype=torch.bfloat16, device=dev)
+    with _on(dev):
+        ws = torch.empty(S * B * Rp, dtype=torch.float32, device=dev)
+        check(lib.tans_fp8_gemm_fused(_ptr(m.comp), m.comp.numel(), _ptr(m.offsets),
+                                      _ptr(m.states), _ptr(m.sm), _ptr(decode_tbl), log2L, R, C,
+                                      S, Nc, _ptr(x2), B, float(scale), _ptr(ws), ws.numel() * 4,
+                                      _ptr(y), _stream(dev)), "fp8_gemm_fused_tans")
+    return y.view(R) if squeeze else y
+
+
+def fp8_gemm_raw(W: torch.Tensor, x: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """The same product from uncompressed FP8 bytes W [R, C] (C % 16 == 0)."""
+    _check_dev("W", W, torch.uint8)
+    _require(W.dim() == 2 and W.shape[1] % 16 == 0, "W must be [R, C] with C % 16 == 0")
+    R, C = W.shape
+    x2, B, squeeze = _batch_view(x, C)
+    _require(x2.device == W.device, "W and x must be on one device")
+    y = torch.empty((B, R), dtype=torch.bfloat16, device=W.device)
+    with _on(W.device):
+        check(lib.tans_fp8_gemm_raw(_ptr(W), R, C, _ptr(x2), B, float(scale), _ptr(y),
+                                    _stream(W.device)), "fp8_gemm_raw")
+    return y.view(R) if squeeze else y

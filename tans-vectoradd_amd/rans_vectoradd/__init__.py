@@ -1,6 +1,8 @@
 """MI355X (gfx950) fused tANS FP8 decode: drop-in for the reference's
 ``rans_vectoradd`` package (rans_vectoradd/__init__.py:1-18)."""
 from rans_vectoradd._C import (
+    fp8_gemm_fused_tans,
+    fp8_gemm_raw,
     fp8_memcpy,
     fp8_vecadd_fused_tans,
     fp8_vecadd_raw,
@@ -11,6 +13,8 @@ from . import tans_codec
 
 __all__ = [
     "QWEN3_14B_FP8_EXP",
+    "fp8_gemm_fused_tans",
+    "fp8_gemm_raw",
     "fp8_memcpy",
     "fp8_vecadd_fused_tans",
     "fp8_vecadd_raw",

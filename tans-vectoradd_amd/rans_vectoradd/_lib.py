@@ -24,10 +24,14 @@ EXPORTS = (
     "tans_build_decode_table_device",
     "tans_fp8_vecadd_fused",
     "tans_decode",
+    "tans_fp8_gemm_fused",
+    "tans_fp8_gemm_raw",
 )
 
 TANS_LANES = 64
 TANS_TILE = 16
+TANS_GEMM_MAX_BATCH = 8
+TANS_GEMM_MAX_SEG_COLS = 512
 TANS_PAIR_LOG2L = 12
 TANS_NIBBLE_LOG2L = 11
 
@@ -56,6 +60,9 @@ for _name, _args in {
     "tans_fp8_vecadd_fused": [_P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I32,
                               _I64, _I64, _P, _P],
     "tans_decode": [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I64, _P, _P],
+    "tans_fp8_gemm_fused": [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _I64,
+                            ctypes.c_float, _P, _I64, _P, _P],
+    "tans_fp8_gemm_raw": [_P, _I64, _I64, _P, _I64, ctypes.c_float, _P, _P],
 }.items():
     getattr(lib, _name).restype = ctypes.c_int
     getattr(lib, _name).argtypes = _args

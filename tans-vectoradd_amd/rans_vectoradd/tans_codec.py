@@ -15,12 +15,14 @@ The encoded layout (wave64 lane groups, one shared word stream per group,
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 
 import numpy as np
 import torch
 
 from . import _C
-from ._lib import TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PAIR_LOG2L, check, lib
+from ._lib import (TANS_GEMM_MAX_SEG_COLS, TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PAIR_LOG2L,
+                   check, lib)
 
 PAIR_L = 1 << TANS_PAIR_LOG2L
 NIBBLE_L = 1 << TANS_NIBBLE_LOG2L
@@ -175,3 +177,89 @@ def compressed_bytes(comp, states, offsets, partial, sm) -> int:
     does (bench_vecadd.py:75-78): payload + sign/mantissa + metadata."""
     return (comp.numel() + sm.numel() + states.numel() * 2 + offsets.numel()
             * offsets.element_size() + partial.numel())
+
+
+# ---------------------------------------------------------------------------
+# Weight matrices for the fused decode-GEMM (no counterpart in the reference)
+# ---------------------------------------------------------------------------
+
+GEMM_BLOCK_ROW_GROUPS = 32    # 64-row groups per workgroup of the GEMM kernel
+GEMM_TARGET_BLOCKS = 256      # workgroups that fill MI355X once (one per CU)
+
+
+@dataclasses.dataclass
+class TansMatrix:
+    """A tANS-coded FP8 matrix W [rows, cols] in the layout the fused GEMM
+    reads (see encode_matrix).  The tensors are the encode() 7-tuple of the
+    slab view; ``to`` moves them to a device."""
+    comp: torch.Tensor
+    states: torch.Tensor
+    offsets: torch.Tensor
+    partial: torch.Tensor
+    sm: torch.Tensor
+    freqs: torch.Tensor
+    spread: torch.Tensor
+    rows: int
+    cols: int
+    segments: int
+    seg_cols: int
+    alphabet: str
+
+    def to(self, device) -> "TansMatrix":
+        moved = {f.name: getattr(self, f.name).to(device)
+                 for f in dataclasses.fields(self) if isinstance(getattr(self, f.name), torch.Tensor)}
+        return dataclasses.replace(self, **moved)
+
+    def decode_table(self) -> torch.Tensor:
+        return build_decode_table(self.spread.cpu().numpy(), self.freqs.cpu().numpy())
+
+    def compressed_bytes(self) -> int:
+        return compressed_bytes(self.comp, self.states, self.offsets, self.partial, self.sm)
+
+
+def gemm_segments(rows: int, cols: int) -> int:
+    """Default column-segment count: enough segments that segments x
+    workgroups-per-segment fills the GPU once, but segments of at least 16
+    and at most 512 columns."""
+    row_groups = -(-rows // TANS_LANES)
+    blocks_per_seg = -(-row_groups // GEMM_BLOCK_ROW_GROUPS)
+    s = min(max(1, GEMM_TARGET_BLOCKS // blocks_per_seg), max(1, cols // 16))
+    return max(s, -(-cols // TANS_GEMM_MAX_SEG_COLS))
+
+
+def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None,
+                  alphabet: str = "pair") -> TansMatrix:
+    """tANS-encode an FP8 matrix [R, C] for fp8_gemm_fused_tans.
+
+    Rows are padded to Rp (a multiple of 64) and columns to S * Nc, Nc even
+    and at most 512; segment s holds columns [s Nc, (s + 1) Nc).  The slab
+    view [S * Rp, Nc] (lane s * Rp + r = row r of segment s) is encoded with
+    encode(), so a 64-lane group is 64 rows of one segment.  Padding bytes
+    hold the most frequent exponent (a finite value with a nonzero
+    frequency); the kernel multiplies them by zero."""
+    if not (isinstance(w_fp8, torch.Tensor) and w_fp8.dim() == 2 and w_fp8.dtype == torch.uint8):
+        raise ValueError("w_fp8 must be a 2-D uint8 tensor [R, C]")
+    R, C = w_fp8.shape
+    if R == 0 or C == 0:
+        raise ValueError("empty matrix")
+    S = segments if segments is not None else gemm_segments(R, C)
+    if S < 1:
+        raise ValueError("segments must be >= 1")
+    Nc = -(-C // S)
+    Nc += Nc % 2
+    if Nc > TANS_GEMM_MAX_SEG_COLS:
+        raise ValueError(f"segments of {Nc} columns exceed {TANS_GEMM_MAX_SEG_COLS}; use more segments")
+    S = -(-C // Nc)                       # (S - 1) * Nc < C <= S * Nc
+    Rp = -(-R // TANS_LANES) * TANS_LANES
+    if isinstance(exp_freqs, torch.Tensor):
+        exp_freqs = exp_freqs.detach().cpu().double().numpy()
+    pad = int(np.argmax(np.asarray(exp_freqs, dtype=np.float64))) << 3
+    w = w_fp8.cpu()
+    if Rp != R or S * Nc != C:
+        wp = torch.full((Rp, S * Nc), pad, dtype=torch.uint8)
+        wp[:R, :C] = w
+        w = wp
+    slab = w.view(Rp, S, Nc).permute(1, 0, 2).reshape(S * Rp, Nc).contiguous()
+    comp, states, offsets, partial, sm, freqs, spread = encode(slab, exp_freqs, alphabet=alphabet)
+    return TansMatrix(comp, states, offsets, partial, sm, freqs, spread, rows=R, cols=C,
+                      segments=S, seg_cols=Nc, alphabet=alphabet)

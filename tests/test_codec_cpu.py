@@ -211,3 +211,41 @@ def test_untile_inverts_the_tiled_layout(T):
     x = torch.arange(K * N, dtype=torch.int64).reshape(K, N)
     tiled = x.reshape(K, N // 16, 16).permute(1, 0, 2).reshape(-1)
     assert torch.equal(T.untile(tiled, K, N), x)
+
+
+@pytest.mark.parametrize("alphabet", list(ALPHABETS))
+@pytest.mark.parametrize("R,C,S", [(17408 // 16, 5120 // 16, None), (100, 70, None), (64, 512, 1),
+                                   (130, 1000, 3), (5, 17, 2)])
+def test_encode_matrix_slab_layout(T, alphabet, R, C, S):
+    """encode_matrix: rows padded to 64, columns to S * Nc (Nc even, at most
+    512), segment s of row r at lane s * Rp + r; the oracle decodes the
+    encoding back to exactly that padded slab view."""
+    from rans_vectoradd import data as D
+    q, _ = D.gaussian_fp8_bytes(R * C, seed=R + C)
+    w = q.reshape(R, C)
+    hist = D.exp_histogram(q)
+    m = T.encode_matrix(w, hist, segments=S, alphabet=alphabet)
+    Rp = -(-R // 64) * 64
+    Nc = m.seg_cols
+    assert Nc % 2 == 0 and Nc <= 512
+    assert (m.segments - 1) * Nc < C <= m.segments * Nc
+    if S is not None:
+        assert m.segments <= S
+    log2L, sps = ALPHABETS[alphabet]
+    K = m.segments * Rp
+    dec = O.w64_decode(m.comp.numpy(), m.offsets.numpy(), m.states.numpy(), m.sm.numpy(),
+                       m.spread.numpy(), m.freqs.numpy(), log2L, sps, K, Nc)
+    slab = dec.reshape(m.segments, Rp, Nc).transpose(1, 0, 2).reshape(Rp, m.segments * Nc)
+    assert np.array_equal(slab[:R, :C], w.numpy())
+    pad = int(np.argmax(hist.numpy())) << 3
+    assert (slab[R:, :] == pad).all() and (slab[:, C:] == pad).all()
+
+
+def test_encode_matrix_rejects_bad_input(T):
+    from rans_vectoradd import data as D
+    with pytest.raises(ValueError):
+        T.encode_matrix(torch.zeros(16, dtype=torch.uint8), D.QWEN3_14B_FP8_EXP)
+    with pytest.raises(ValueError):
+        T.encode_matrix(torch.zeros((4, 2000), dtype=torch.uint8), D.QWEN3_14B_FP8_EXP, segments=1)
+    with pytest.raises(ValueError):
+        T.encode_matrix(torch.zeros((0, 16), dtype=torch.uint8), D.QWEN3_14B_FP8_EXP)

@@ -1,0 +1,132 @@
+"""GPU tests of the fused decode + skinny GEMM (no
+reference counterpart): y = scale * (W @ x^T) with W tANS-coded, checked
+against a float64 product of the same FP8 weights and bf16 activations
+(tolerance 1e-2 relative: |y - y_ref| <= 1e-2 |y_ref| + 1e-3 max|y_ref|
+per element, which also bounds max|y - y_ref| / max|y_ref| by 1.1e-2), and
+against the uncompressed FP8 kernel."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+REL, FLOOR = 1e-2, 1e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def R():
+    import rans_vectoradd
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return rans_vectoradd
+
+
+def _weights(rows, cols, seed, dist="gaussian"):
+    from rans_vectoradd import data as D
+    gen = D.gaussian_fp8_bytes if dist == "gaussian" else D.laplace_fp8_bytes
+    q, scale = gen(rows * cols, seed=seed)
+    return q.reshape(rows, cols), scale
+
+
+def _x(B, cols, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(B, cols, generator=g).to(torch.bfloat16)
+
+
+def _reference(w_u8, x_bf16, scale):
+    w = w_u8.view(torch.float8_e4m3fn).to(torch.float64)
+    return scale * (x_bf16.to(torch.float64) @ w.t())
+
+
+def _check(y, ref):
+    y = y.cpu().to(torch.float64)
+    err = (y - ref).abs()
+    bound = REL * ref.abs() + FLOOR * ref.abs().max()
+    assert bool((err <= bound).all()), f"max err {err.max().item():.3e}, max|ref| {ref.abs().max().item():.3e}"
+    assert err.max().item() <= 1.1e-2 * ref.abs().max().item()
+
+
+def _fused(R, m, x, scale):
+    from rans_vectoradd import tans_codec as T
+    md = m.to("cuda")
+    tbl = m.decode_table().cuda()
+    return R.fp8_gemm_fused_tans(md, tbl, x.cuda(), scale)
+
+
+@pytest.mark.parametrize("alphabet", ["pair", "nibble"])
+@pytest.mark.parametrize("rows,cols,B,segments", [(2176, 1280, 1, None), (2176, 1280, 3, None),
+                                                  (2176, 1280, 8, None), (100, 70, 2, None),
+                                                  (130, 1000, 5, 3), (64, 512, 4, 1),
+                                                  (5, 18, 7, None)])
+def test_gemm_fused_vs_float64(R, alphabet, rows, cols, B, segments):
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: fp8_gemm_fused_tans {rows}x{cols} B={B} S={segments} {alphabet}")
+    w, scale = _weights(rows, cols, seed=rows + cols)
+    x = _x(B, cols, seed=B)
+    m = T.encode_matrix(w, D.exp_histogram(w), segments=segments, alphabet=alphabet)
+    y = _fused(R, m, x, scale)
+    assert y.shape == (B, rows) and y.dtype == torch.bfloat16
+    _check(y, _reference(w, x, scale))
+
+
+def test_gemm_fused_vector_input_and_determinism(R):
+    from rans_vectoradd import data as D, tans_codec as T
+    _say("case: fp8_gemm_fused_tans vector x, repeated calls")
+    w, scale = _weights(640, 960, seed=3)
+    x = _x(1, 960, seed=4)[0]
+    m = T.encode_matrix(w, D.exp_histogram(w))
+    md, tbl = m.to("cuda"), m.decode_table().cuda()
+    y1 = R.fp8_gemm_fused_tans(md, tbl, x.cuda(), scale)
+    y2 = R.fp8_gemm_fused_tans(md, tbl, x.cuda(), scale)
+    assert y1.shape == (640,)
+    assert torch.equal(y1, y2)
+    _check(y1.view(1, -1), _reference(w, x.view(1, -1), scale))
+
+
+@pytest.mark.parametrize("rows,cols,B", [(2176, 1280, 1), (2176, 1280, 8), (100, 64, 3),
+                                         (5120, 17408 // 4, 2)])
+def test_gemm_raw_vs_float64(R, rows, cols, B):
+    _say(f"case: fp8_gemm_raw {rows}x{cols} B={B}")
+    w, scale = _weights(rows, cols, seed=7)
+    x = _x(B, cols, seed=8)
+    y = R.fp8_gemm_raw(w.cuda(), x.cuda(), scale)
+    _check(y, _reference(w, x, scale))
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_gemm_config3_shape_fused_vs_raw(R, B):
+    """Config 3's W_up shape (17408 x 5120) and config 4's mismatched-table
+    case (a table from a Laplace histogram): both match float64, and the
+    fused and raw kernels agree to a bf16 rounding step."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: gemm 17408x5120 B={B}")
+    w, scale = _weights(17408, 5120, seed=11)
+    x = _x(B, 5120, seed=12)
+    ref = _reference(w, x, scale)
+    raw = R.fp8_gemm_raw(w.cuda(), x.cuda(), scale)
+    _check(raw, ref)
+    lap, _ = D.laplace_fp8_bytes(1 << 20, seed=13)
+    for hist in (D.exp_histogram(w), D.exp_histogram(lap)):
+        m = T.encode_matrix(w, hist)
+        y = _fused(R, m, x, scale)
+        _check(y, ref)
+        d = (y.float() - raw.float()).abs()
+        assert bool((d <= 2.0 ** -7 * raw.float().abs() + 1e-6).all())
+
+
+def test_gemm_argument_errors(R):
+    from rans_vectoradd import data as D, tans_codec as T
+    w, scale = _weights(64, 32, seed=1)
+    m = T.encode_matrix(w, D.exp_histogram(w))
+    md, tbl = m.to("cuda"), m.decode_table().cuda()
+    with pytest.raises(RuntimeError):
+        R.fp8_gemm_fused_tans(md, tbl, _x(9, 32, 0).cuda(), scale)       # batch > 8
+    with pytest.raises(RuntimeError):
+        R.fp8_gemm_fused_tans(md, tbl, _x(1, 31, 0).cuda(), scale)       # wrong width
+    with pytest.raises(RuntimeError):
+        R.fp8_gemm_fused_tans(md, tbl, _x(1, 32, 0).float().cuda(), scale)   # not bf16
+    with pytest.raises(RuntimeError):
+        R.fp8_gemm_raw(torch.zeros(4, 24, dtype=torch.uint8).cuda(), _x(1, 24, 0).cuda())
