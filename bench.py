@@ -62,6 +62,7 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-sweep", action="store_true", help="headline config only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-decode", action="store_true", help="skip config 2 (standalone decode)")
+    p.add_argument("--no-gemm", action="store_true", help="skip configs 3-4 (decode-GEMV/GEMM)")
     p.add_argument("--alphabet", choices=("pair", "nibble"), default="pair",
                    help="alphabet of --profile fused/decode")
     p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode"),
@@ -209,6 +210,150 @@ def run_decode_config(dist: str, alphabet: str, seed: int, steps: int, warmup: i
             "call_ms": kernel_ms, "step_ms": step_ms,
             "eff_gbs": 2 * n / (step_ms * 1e-3) / 1e9,
             "hbm_gbs": (in_bytes + n) / (step_ms * 1e-3) / 1e9}
+
+
+GEMM_UP = (17408, 5120)              # configs 3-4: W_up; W_down is the transpose shape
+GEMM_LAYERS = 40
+GEMV_COPIES = 4                      # rotated so the 256 MB MALL cannot hold W
+
+
+def graph_timed(fn, reps: int, steps: int, warmup: int, settle_s: float):
+    """Capture `reps` calls of fn in one HIP graph (no host launch cost in
+    the timed part) and time its replays with timed(); returns per-call
+    (kernel ms, step ms), the graph's outputs and the eager outputs of the
+    same calls, so the caller can check every replay against eager work."""
+    import torch
+    eager = [fn() for _ in range(reps)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # a whole cycle, so a stateful fn restarts in step
+        for _ in range(reps):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [fn() for _ in range(reps)]
+    kernel_ms, step_ms = timed(g.replay, steps, warmup, settle_s)
+    torch.cuda.synchronize()
+    same = all(torch.equal(a, b) for a, b in zip(outs, eager))
+    return kernel_ms / reps, step_ms / reps, same
+
+
+def gemm_matrix(rows: int, cols: int, seed: int, table_hist=None, alphabet: str = "pair"):
+    """A config-3 weight matrix (N(0, 0.02), per-tensor scale to 448, RNE
+    E4M3FN) generated on the GPU; returns (raw bytes on the GPU, scale,
+    encoded TansMatrix on the GPU, its decode table).  table_hist: the
+    exponent histogram the table is built from (default: the data's own)."""
+    from rans_vectoradd import data as D, tans_codec as T
+    q, scale = D.gaussian_fp8_bytes(rows * cols, seed=seed, device="cuda")
+    w = q.view(rows, cols)
+    hist = D.exp_histogram(q).cpu() if table_hist is None else table_hist
+    m = T.encode_matrix(w.cpu(), hist, alphabet=alphabet)
+    return w, scale, m.to("cuda"), m.decode_table().cuda()
+
+
+def run_gemv_config(seed: int, steps: int, warmup: int, settle_s: float) -> dict:
+    """Config 3: y = scale * (W x), W 17408 x 5120 tANS-coded, x bf16 [5120],
+    against the uncompressed FP8 kernel; GEMV_COPIES copies of W rotate."""
+    import torch
+    import rans_vectoradd as R
+
+    rows, cols = GEMM_UP
+    mats = [gemm_matrix(rows, cols, seed + 100 + i) for i in range(GEMV_COPIES)]
+    gx = torch.Generator(device="cuda").manual_seed(seed + 99)
+    x = torch.randn(cols, generator=gx, device="cuda").to(torch.bfloat16)
+    it = [0, 0]
+
+    def fused():
+        w, sc, m, tbl = mats[it[0] % GEMV_COPIES]
+        it[0] += 1
+        return R.fp8_gemm_fused_tans(m, tbl, x, sc)
+
+    def raw():
+        w, sc, m, tbl = mats[it[1] % GEMV_COPIES]
+        it[1] += 1
+        return R.fp8_gemm_raw(w, x, sc)
+
+    yf = torch.stack([fused() for _ in range(GEMV_COPIES)]).float()
+    yr = torch.stack([raw() for _ in range(GEMV_COPIES)]).float()
+    max_rel = float((yf - yr).abs().max() / yr.abs().max())
+    f_ms, f_step, f_same = graph_timed(fused, 4 * GEMV_COPIES, steps, warmup, settle_s)
+    r_ms, r_step, r_same = graph_timed(raw, 4 * GEMV_COPIES, steps, warmup, settle_s)
+    comp = sum(m.compressed_bytes() for _, _, m, _ in mats) / GEMV_COPIES
+    io = cols * 2 + rows * 2
+    out = {"shape": [rows, cols], "batch": 1, "copies": GEMV_COPIES,
+           "bits_per_byte": comp * 8 / (rows * cols),
+           "fused_us": f_step * 1e3, "raw_us": r_step * 1e3, "x_raw": r_step / f_step,
+           "fused_hbm_gbs": (comp + io) / (f_step * 1e-3) / 1e9,
+           "raw_hbm_gbs": (rows * cols + io) / (r_step * 1e-3) / 1e9,
+           "max_rel_diff_vs_raw": max_rel, "graph_replays_match_eager": f_same and r_same}
+    del mats
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_gemm_config(seed: int, batches, steps: int, warmup: int, settle_s: float) -> dict:
+    """Config 4: GEMM_LAYERS layers of W_up [17408, 5120] and W_down
+    [5120, 17408]; per layer h = W_up x, y = W_down h for X bf16 [B, 5120].
+    Layers in the second half are encoded with a table from a
+    Laplace(0, 0.015) histogram (mismatched to their Gaussian data).  A pass
+    over all layers is one HIP graph."""
+    import torch
+    import rans_vectoradd as R
+    from rans_vectoradd import data as D
+
+    lap, _ = D.laplace_fp8_bytes(1 << 24, seed=seed + 7)
+    lap_hist = D.exp_histogram(lap)
+    rows, cols = GEMM_UP
+    layers = []
+    for i in range(GEMM_LAYERS):
+        hist = None if i < GEMM_LAYERS // 2 else lap_hist
+        up = gemm_matrix(rows, cols, seed + 1000 + 2 * i, hist)
+        down = gemm_matrix(cols, rows, seed + 1001 + 2 * i, hist)
+        layers.append((up, down))
+    half = GEMM_LAYERS // 2
+
+    def bits(ls):
+        b = sum(u[2].compressed_bytes() + d[2].compressed_bytes() for u, d in ls)
+        return b * 8 / (len(ls) * 2 * rows * cols)
+
+    comp = sum(u[2].compressed_bytes() + d[2].compressed_bytes() for u, d in layers)
+    raw_bytes = GEMM_LAYERS * 2 * rows * cols
+    res = {"layers": GEMM_LAYERS, "shapes": [[rows, cols], [cols, rows]],
+           "bits_per_byte_matched": bits(layers[:half]),
+           "bits_per_byte_mismatched": bits(layers[half:]), "batches": []}
+    for B in batches:
+        gx = torch.Generator(device="cuda").manual_seed(seed + B)
+        X = torch.randn(B, cols, generator=gx, device="cuda").to(torch.bfloat16)
+
+        def fused_pass(layers=layers, X=X):
+            outs = []
+            for (wu, su, mu, tu), (wd, sd, md, td) in layers:
+                h = R.fp8_gemm_fused_tans(mu, tu, X, su)
+                outs.append(R.fp8_gemm_fused_tans(md, td, h, sd))
+            return torch.stack(outs)
+
+        def raw_pass(layers=layers, X=X):
+            outs = []
+            for (wu, su, mu, tu), (wd, sd, md, td) in layers:
+                h = R.fp8_gemm_raw(wu, X, su)
+                outs.append(R.fp8_gemm_raw(wd, h, sd))
+            return torch.stack(outs)
+
+        yf, yr = fused_pass().float(), raw_pass().float()
+        rel = float(((yf - yr).abs().amax(dim=(1, 2)) / yr.abs().amax(dim=(1, 2))).max())
+        f_ms, f_step, f_same = graph_timed(fused_pass, 1, max(steps // 10, 5), 2, settle_s)
+        r_ms, r_step, r_same = graph_timed(raw_pass, 1, max(steps // 10, 5), 2, settle_s)
+        res["batches"].append({
+            "batch": B, "fused_ms_per_pass": f_step, "raw_ms_per_pass": r_step,
+            "x_raw": r_step / f_step, "fused_hbm_gbs": comp / (f_step * 1e-3) / 1e9,
+            "raw_hbm_gbs": raw_bytes / (r_step * 1e-3) / 1e9, "max_rel_diff_vs_raw": rel,
+            "graph_replays_match_eager": f_same and r_same})
+        log(f"  gemm B={B}: fused {f_step:.3f} ms  raw {r_step:.3f} ms  x_raw "
+            f"{r_step / f_step:.3f}  rel diff {rel:.2e}")
+    del layers
+    torch.cuda.empty_cache()
+    return res
 
 
 def read_traffic():
@@ -398,6 +543,15 @@ def main() -> None:
                 log(f"  call {r['step_ms'] * 1e3:.1f} us  eff {r['eff_gbs']:.0f} GB/s  "
                     f"hbm {r['hbm_gbs']:.0f} GB/s  bits/B {r['bits_per_byte']:.3f}  "
                     f"exact {r['exact']}")
+    if not args.no_gemm:
+        log("gemv: config 3")
+        line["gemv"] = run_gemv_config(args.seed, args.steps, args.warmup, args.settle)
+        g = line["gemv"]
+        log(f"  fused {g['fused_us']:.1f} us  raw {g['raw_us']:.1f} us  x_raw {g['x_raw']:.3f}  "
+            f"bits/B {g['bits_per_byte']:.3f}  rel diff {g['max_rel_diff_vs_raw']:.2e}")
+        log("gemm: config 4")
+        line["gemm"] = run_gemm_config(args.seed, (1, 2, 4, 8), args.steps, args.warmup,
+                                       args.settle)
     if not args.no_cpu:
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(args.seed)
