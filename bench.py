@@ -65,7 +65,7 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-gemm", action="store_true", help="skip configs 3-4 (decode-GEMV/GEMM)")
     p.add_argument("--alphabet", choices=("pair", "nibble"), default="pair",
                    help="alphabet of --profile fused/decode")
-    p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode"),
+    p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode", "gemv", "gemv_raw"),
                    help="only launch this kernel --steps times (for rocprofv3)")
     return p.parse_args()
 
@@ -433,7 +433,15 @@ def profile_only(args) -> None:
     import rans_vectoradd as R
     from rans_vectoradd import tans_codec as T
 
-    if args.profile == "decode":   # config 2: 2^30 Gaussian elements, 1024 per lane
+    if args.profile in ("gemv", "gemv_raw"):   # config 3, one W (it stays MALL-resident)
+        gx = torch.Generator(device="cuda").manual_seed(args.seed + 99)
+        w, sc, m, tbl = gemm_matrix(*GEMM_UP, args.seed + 100, alphabet=args.alphabet)
+        x = torch.randn(GEMM_UP[1], generator=gx, device="cuda").to(torch.bfloat16)
+        if args.profile == "gemv":
+            fn = lambda: R.fp8_gemm_fused_tans(m, tbl, x, sc)   # noqa: E731
+        else:
+            fn = lambda: R.fp8_gemm_raw(w, x, sc)               # noqa: E731
+    elif args.profile == "decode":   # config 2: 2^30 Gaussian elements, 1024 per lane
         from rans_vectoradd import data as D
         K = DECODE_ELEMS // HEADLINE_LANE
         q, _ = D.gaussian_fp8_bytes(DECODE_ELEMS, seed=args.seed, device="cuda")

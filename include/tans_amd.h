@@ -150,7 +150,7 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
  *   workspace  device memory of at least S * B * Rp * 4 bytes (per-segment
  *              fp32 partial sums; contents on entry do not matter)
  *   y          bf16 [B, R]
- * Partial sums are added in segment order, so results are deterministic. */
+ * Partial sums are added in a fixed order, so results are deterministic. */
 int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* offsets,
                         const uint16_t* states, const void* sm, const uint32_t* table,
                         int32_t log2L, int64_t R, int64_t C, int64_t S, int64_t Nc,

@@ -802,8 +802,8 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
 // lane become 8 bf16 pairs (exact) that meet x in v_dot2_f32_bf16 with
 // fp32 accumulation; x is read once per tile and batch row with a
 // wave-uniform LDS address (a broadcast).  Partial sums go to a workspace
-// [S][B][Rp] and gemm_finalize_kernel adds the S segments in order, scales
-// and rounds to bf16 (round to nearest even).
+// [S][B][Rp] and gemm_finalize_kernel adds the S segments in a fixed
+// order, scales and rounds to bf16 (round to nearest even).
 // ---------------------------------------------------------------------
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 constexpr int kGemmChains = 2;                        // row groups per wave
@@ -975,16 +975,31 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
     return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
-// y[b][r] = bf16(scale * sum over s of ws[s][b][r]), s in ascending order.
-__global__ __launch_bounds__(256) void gemm_finalize_kernel(const float* __restrict__ ws, int S,
-                                                            int NB, int64_t Rp, int64_t R,
-                                                            float scale, uint16_t* __restrict__ y) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= (int64_t)NB * R) return;
-    const int64_t b = i / R, r = i % R;
+// y[b][r] = bf16(scale * sum over s of ws[s][b][r]).  A block of 4 waves
+// takes 64 consecutive outputs of one batch row: wave w sums segments
+// s = w, w + 4, ... in ascending order (coalesced 256-byte loads), and the
+// four sums are added in wave order, so the result is deterministic.
+constexpr int kFinWaves = 4;
+
+__global__ __launch_bounds__(kFinWaves * kLanes) void gemm_finalize_kernel(
+    const float* __restrict__ ws, int S, int NB, int64_t Rp, int64_t R, float scale,
+    uint16_t* __restrict__ y) {
+    __shared__ float part[kFinWaves][kLanes];
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int wave = threadIdx.x / kLanes;
+    const int64_t blocks_per_b = (R + kLanes - 1) / kLanes;
+    const int64_t b = blockIdx.x / blocks_per_b;
+    const int64_t r = (blockIdx.x % blocks_per_b) * kLanes + lane;   // < Rp: Rp is a multiple of 64
     float a = 0.0f;
-    for (int s = 0; s < S; s++) a += ws[((int64_t)s * NB + b) * Rp + r];
-    y[i] = bf16_rne(a * scale);
+    for (int s = wave; s < S; s += kFinWaves) a += ws[((int64_t)s * NB + b) * Rp + r];
+    part[wave][lane] = a;
+    __syncthreads();
+    if (wave == 0 && r < R) {
+        float t = part[0][lane];
+        #pragma unroll
+        for (int w = 1; w < kFinWaves; w++) t += part[w][lane];
+        y[b * R + r] = bf16_rne(t * scale);
+    }
 }
 
 // Uncompressed FP8 skinny GEMM (the baseline of the fused one): a wave
@@ -1201,8 +1216,9 @@ int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* off
 #undef TANS_GEMM_CASE
     int rc = hip_check(hipGetLastError(), "gemm_fused_kernel launch");
     if (rc != TANS_OK) return rc;
-    hipLaunchKernelGGL(gemm_finalize_kernel, dim3((unsigned)((B * R + 255) / 256)), dim3(256), 0,
-                       st, (const float*)workspace, (int)S, (int)B, Rp, R, scale, (uint16_t*)y);
+    hipLaunchKernelGGL(gemm_finalize_kernel, dim3((unsigned)(B * (Rp / kLanes))),
+                       dim3(kFinWaves * kLanes), 0, st, (const float*)workspace, (int)S, (int)B, Rp,
+                       R, scale, (uint16_t*)y);
     return hip_check(hipGetLastError(), "gemm_finalize_kernel launch");
 }
 
