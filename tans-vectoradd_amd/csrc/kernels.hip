@@ -129,69 +129,92 @@ __global__ __launch_bounds__(kBlock) void fp8_add_kernel(const v4u* __restrict__
 }
 
 // ---------------------------------------------------------------------
-// Decode table on the device: one workgroup of 16 waves, wave w owning
-// slots [w L/16, (w+1) L/16) in rounds of 64.  A symbol's rank (its earlier
-// slots in slot order) is its count in earlier waves plus its count earlier
-// in its own wave; the latter is found per round by taking the distinct
-// symbols of the round one at a time (ballot of the lanes holding the
-// first remaining one, mbcnt for each lane's place among them).
+// Decode table on the device: one workgroup of 16 waves.  The L slots are
+// cut into segments of 64 (wave w, round r: segment w * rounds + r, so
+// segments follow slot order).  A symbol's rank (its earlier slots, in
+// slot order) is its count in earlier segments plus its place among equal
+// symbols in its own segment.  The lanes holding a lane's symbol are the
+// AND over symbol bits of that bit's ballot (complemented where the lane's
+// own bit is 0); mbcnt of that mask is the place, its popcount the count,
+// and the last lane holding each symbol writes the count to LDS.  An exclusive prefix over segments (16
+// segments per thread, then 4 partial totals per symbol) gives the rest.
 // ---------------------------------------------------------------------
 constexpr int kTableWaves = 16;
+constexpr int kTableSegs = kTableWaves * 4;   // 64 segments of 64 slots at L = 4096
 
 __global__ __launch_bounds__(kTableWaves * 64) void table_kernel(
     const int32_t* __restrict__ spread, const int32_t* __restrict__ freqs, int nsym, int log2L,
     v2u* __restrict__ table) {
-    __shared__ uint32_t cnt[kTableWaves][256];   // occurrences per wave, then per earlier waves
+    __shared__ uint16_t cnt[kTableSegs][256];   // per segment: counts, then exclusive prefix
+    __shared__ uint16_t tot[4][256];            // prefix totals of segment quarters
     const uint32_t L = 1u << log2L;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    for (uint32_t i = threadIdx.x; i < kTableWaves * 256; i += blockDim.x) (&cnt[0][0])[i] = 0;
+    const int rounds = (int)(L / (kTableWaves * 64));   // 4 (pair) or 2 (nibble)
+    const int sym_bits = 31 - __builtin_clz((uint32_t)nsym);
+    const int nseg = kTableWaves * rounds;
+    for (uint32_t i = threadIdx.x; i < kTableSegs * 256 / 2; i += blockDim.x)
+        reinterpret_cast<uint32_t*>(&cnt[0][0])[i] = 0u;
     __syncthreads();
-    const uint32_t per_wave = L / kTableWaves;      // 256 (pair) or 128 (nibble) slots
-    const int rounds = (int)(per_wave / 64);
     uint32_t sym[4] = {0u, 0u, 0u, 0u}, rank[4] = {0u, 0u, 0u, 0u};
     #pragma unroll
     for (int r = 0; r < 4; r++) {
         if (r >= rounds) break;
-        const uint32_t slot = wave * per_wave + (uint32_t)r * 64 + lane;
+        const int seg = wave * rounds + r;
         // a symbol outside the alphabet is folded into it: a wrong table,
         // never an out-of-range access (the host builder rejects such input)
-        const uint32_t s = (uint32_t)spread[slot] & (uint32_t)(nsym - 1);
-        sym[r] = s;
-        uint64_t todo = __ballot(true);
-        while (todo) {   // wave-uniform
-            const uint32_t first = (uint32_t)__builtin_ctzll(todo);
-            const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)s, (int)first);
-            const uint64_t m = __ballot(s == s0);
-            const uint32_t before = cnt[wave][s0];
-            if (s == s0)
-                rank[r] = before + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-            if (lane == (int)first) cnt[wave][s0] = before + (uint32_t)__popcll(m);
-            todo &= ~m;
+        const uint32_t sv = (uint32_t)spread[seg * 64 + lane] & (uint32_t)(nsym - 1);
+        sym[r] = sv;
+        // the lanes holding the same symbol: for each symbol bit, the ballot
+        // of lanes with that bit set, complemented where this lane's bit is 0
+        uint32_t mlo = 0xFFFFFFFFu, mhi = 0xFFFFFFFFu;
+        #pragma unroll
+        for (int bit = 0; bit < 8; bit++) {
+            if (bit >= sym_bits) break;
+            const uint64_t B = __ballot((sv >> bit) & 1u);
+            const uint32_t mine = (uint32_t)__builtin_amdgcn_sbfe((int)sv, bit, 1);   // 0 or ~0
+            mlo &= ~((uint32_t)B ^ mine);
+            mhi &= ~((uint32_t)(B >> 32) ^ mine);
         }
+        const uint32_t rk = __builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
+        const uint32_t tot = (uint32_t)__builtin_popcount(mlo) + (uint32_t)__builtin_popcount(mhi);
+        rank[r] = rk;
+        if (rk + 1u == tot) cnt[seg][sv] = (uint16_t)tot;
     }
     __syncthreads();
-    if (threadIdx.x < (unsigned)nsym) {            // exclusive prefix over the waves
-        uint32_t run = 0;
-        for (int w = 0; w < kTableWaves; w++) {
-            const uint32_t c = cnt[w][threadIdx.x];
-            cnt[w][threadIdx.x] = run;
+    // exclusive prefix over segments: thread (q, s) scans segments [16q, 16q + 16)
+    const int s = threadIdx.x & 255;
+    const int q = threadIdx.x >> 8;
+    uint32_t run = 0;
+    if (s < nsym) {
+        uint16_t v[16];
+        #pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = (16 * q + i < nseg) ? cnt[16 * q + i][s] : (uint16_t)0;
+        #pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t c = v[i];
+            v[i] = (uint16_t)run;
             run += c;
         }
+        tot[q][s] = (uint16_t)run;
+        #pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (16 * q + i < nseg) cnt[16 * q + i][s] = v[i];
     }
     __syncthreads();
     #pragma unroll
     for (int r = 0; r < 4; r++) {
         if (r >= rounds) break;
-        const uint32_t s = sym[r];
-        const uint32_t slot = wave * per_wave + (uint32_t)r * 64 + lane;
-        const uint32_t xp = (uint32_t)freqs[s] + cnt[wave][s] + rank[r];
+        const int seg = wave * rounds + r;
+        const uint32_t sv = sym[r];
+        uint32_t before = 0;
+        for (int qq = 0; qq < (seg >> 4); qq++) before += tot[qq][sv];
+        const uint32_t xp = (uint32_t)freqs[sv] + before + cnt[seg][sv] + rank[r];
         const int top = xp ? 31 - __builtin_clz(xp) : log2L;
         const int nb = top < log2L ? log2L - top : 0;
         const uint32_t base = xp << nb;
-        const uint32_t ex = (nsym == 256) ? (((s >> 4) << 11) | ((s & 0xFu) << 19)) : (s << 11);
-        table[slot] = v2u{(uint32_t)nb | ex, (base - L) * 8u};
+        const uint32_t ex = (nsym == 256) ? (((sv >> 4) << 11) | ((sv & 0xFu) << 19)) : (sv << 11);
+        table[seg * 64 + lane] = v2u{(uint32_t)nb | ex, (base - L) * 8u};
     }
 }
 
