@@ -97,6 +97,13 @@ int tans_encode_finish(void* handle, uint8_t* comp, uint16_t* states,
                        int64_t* offsets);
 void tans_encode_free(void* handle);
 
+/* Encode tables of (spread, freqs) for the GPU encoder: enc_tab [nsym] =
+ * f_s | start_s << 16 (start_s = f_0 + ... + f_{s-1}), enc_next [2^log2L]
+ * = L + slot of the rank-th occurrence of s at index start_s + rank.  The
+ * tables the CPU encoder builds internally (tans_encode_begin).          */
+int tans_build_encode_table(const int32_t* spread, const int32_t* freqs, int32_t nsym,
+                            int32_t log2L, uint32_t* enc_tab, uint16_t* enc_next);
+
 /* ---------------- GPU side (gfx950) ---------------------------------- */
 
 /* C = A, 16-byte vectors; n % 16 == 0.  Replaces fp8_memcpy,
@@ -135,6 +142,29 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
                 const uint16_t* states, const void* sm,
                 const uint32_t* table, int32_t log2L,
                 int64_t K, int64_t N, void* out, void* stream);
+
+/* GPU encoder: the same bytes as tans_encode_begin/finish + tans_split_fp8
+ * (the reference's tans_encode_interleaved, csrc/tans_codec.cpp:69-196, and
+ * the split of rans_vectoradd/tans_codec.py:109-124), from FP8 bytes already
+ * on the device.  Three calls:
+ *   workspace  bytes of device scratch begin and finish need for [K, N]
+ *   begin      fp8 [K, N] (device, N even), enc_tab/enc_next from
+ *              tans_build_encode_table (device copies), log2L 12 (pair) or
+ *              11 (nibble).  Writes offsets [ceil(K/64) + 1] (int64 words),
+ *              states [K], sm tiles (layout above), and sets *status (device
+ *              int, zero on entry) to TANS_ESYMBOL if a symbol has frequency
+ *              0.  The caller reads offsets[ceil(K/64)] (the stream words)
+ *              and *status after the stream has reached this point.
+ *   finish     writes comp: offsets[last] stream words + 256 zero words;
+ *              comp_bytes = (offsets[last] + 256) * 4.
+ * The workspace must stay untouched between begin and finish.           */
+int tans_gpu_encode_workspace(int64_t K, int64_t N, int32_t log2L, int64_t* workspace_bytes);
+int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t* enc_tab,
+                          const uint16_t* enc_next, int32_t log2L, void* workspace,
+                          int64_t workspace_bytes, int64_t* offsets, uint16_t* states, void* sm,
+                          int32_t* status, void* stream);
+int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* workspace,
+                           const int64_t* offsets, void* comp, int64_t comp_bytes, void* stream);
 
 /* ---------------- Fused decode + skinny GEMM (no counterpart in the
  * reference: its rows a15 / configs 3-4 are new) ----------------------- */

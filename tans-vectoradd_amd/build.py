@@ -1,5 +1,5 @@
 """Build libtans_amd.so in-tree: the CPU codec (g++, OpenMP) and the gfx950
-HIP kernels (hipcc), linked into one shared library next to the Python
+HIP kernels and GPU encoder (hipcc), linked into one shared library next to the Python
 package (rans_vectoradd/libtans_amd.so).
 
     python tans-vectoradd_amd/build.py [--asm]
@@ -47,13 +47,15 @@ def build(asm: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     codec_o = os.path.join(BUILD, "codec.o")
     kern_o = os.path.join(BUILD, "kernels.o")
+    enc_o = os.path.join(BUILD, "encode.o")
     _run(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, "codec.cpp"), "-o", codec_o])
     _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "kernels.hip"), "-o", kern_o])
+    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "encode.hip"), "-o", enc_o])
     if asm:
         _run([HIPCC, *HIP_FLAGS, "--cuda-device-only", "-S",
               os.path.join(CSRC, "kernels.hip"), "-o", os.path.join(BUILD, "kernels.s")])
     tmp = OUT + ".tmp"
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, codec_o, kern_o,
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, codec_o, kern_o, enc_o,
           "-lgomp"])
     os.replace(tmp, OUT)
     return OUT

@@ -184,6 +184,19 @@ int tans_build_decode_table(const int32_t* spread, const int32_t* freqs, int32_t
     return TANS_OK;
 }
 
+int tans_build_encode_table(const int32_t* spread, const int32_t* freqs, int32_t nsym,
+                            int32_t log2L, uint32_t* enc_tab, uint16_t* enc_next) {
+    if (!spread || !freqs || !enc_tab || !enc_next) return fail(TANS_EINVAL, "encode table: null pointer");
+    if (!((nsym == 256 && log2L == TANS_PAIR_LOG2L) || (nsym == 16 && log2L == TANS_NIBBLE_LOG2L)))
+        return fail(TANS_EINVAL, "encode table: need (nsym 256, log2L 12) or (nsym 16, log2L 11)");
+    EncTables t;
+    int rc = build_enc_tables(freqs, nsym, spread, log2L, t);   // validates
+    if (rc) return rc;
+    for (int s = 0; s < nsym; s++) enc_tab[s] = t.freq[(size_t)s] | (t.start[(size_t)s] << 16);
+    for (uint32_t i = 0; i < (1u << log2L); i++) enc_next[i] = (uint16_t)t.next[i];
+    return TANS_OK;
+}
+
 int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_t* freqs,
                       int32_t nsym, const int32_t* spread, int32_t log2L, void** handle,
                       int64_t* comp_bytes, int64_t* n_offsets) {

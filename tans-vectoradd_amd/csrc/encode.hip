@@ -1,0 +1,386 @@
+// gfx950 tANS encoder into the wave64 lane layout (include/tans_amd.h).
+// It writes the same bytes as the CPU encoder in codec.cpp: the same
+// backward tANS construction (csrc/tans_codec.cpp:22-60 of the reference:
+// walk the symbols backwards from x = L, emit the low nb bits that bring x
+// into [f_s, 2 f_s), then x = L + slot of the rank-th occurrence of s), the
+// same per-step bit chunks written forwards LSB-first, and the same refill
+// schedule ordering the words of a group's 64 lanes.
+//
+// Passes (all on the caller's stream):
+//   enc_backward_kernel  one thread per lane: step chunks [S][K] (u16:
+//                        value in bits 11:0, nb in bits 15:12) and the
+//                        initial decoder state
+//   enc_pack_kernel      one wave per group: each lane packs its chunks into
+//                        words [w][K]; the wave replays the refill schedule
+//                        to count the group's stream words (padded to 4)
+//   enc_scan_kernel      exclusive prefix of the group counts -> offsets
+//   enc_interleave_kernel one wave per group: replays the schedule again and
+//                        writes each taken word at offset + handed + rank
+//   enc_sm_kernel        sign/mantissa tiles
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/tans_amd.h"
+
+extern "C" void tans_internal_set_error(const char* msg);  // codec.cpp
+
+namespace {
+
+constexpr int kLanes = 64;
+constexpr int kTile = 16;
+constexpr int kRefillBelow = 24;   // the decoders' refill threshold
+constexpr int64_t kTailWords = 256;
+constexpr int kEncBlock = 256;
+
+int fail(int code, const std::string& msg) {
+    tans_internal_set_error(msg.c_str());
+    return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return TANS_OK;
+    return fail(TANS_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace layout: chunks u16 [S][K], words u32 [max_words][K],
+// nwords u32 [K], glen u32 [G].
+struct WsLayout {
+    int64_t chunks, words, nwords, glen, total;
+};
+
+WsLayout ws_layout(int64_t K, int64_t S, int32_t log2L) {
+    const int64_t G = (K + kLanes - 1) / kLanes;
+    const int64_t max_words = (S * log2L + 31) / 32 + 1;
+    WsLayout l;
+    l.chunks = 0;
+    l.words = align256(S * K * 2);
+    l.nwords = l.words + align256(max_words * K * 4);
+    l.glen = l.nwords + align256(K * 4);
+    l.total = l.glen + align256(G * 4);
+    return l;
+}
+
+// Exponent symbol of step i of lane k: the pair e0 * 16 + e1 of bytes 2i,
+// 2i + 1, or the exponent of byte i.  Both bytes of a pair lie in the same
+// aligned dword (2i is even and so is the row start, N being even); the
+// tensor's last dword, which may end past its `total` bytes, is read bytewise.
+template <int SPS>
+__device__ __forceinline__ uint32_t symbol_at(const uint8_t* __restrict__ fp8, int64_t byte,
+                                              int64_t total) {
+    const int64_t a = byte & ~int64_t(3);
+    uint32_t w;
+    if (a + 4 <= total) {
+        w = *reinterpret_cast<const uint32_t*>(fp8 + a);
+    } else {
+        w = 0;
+        for (int64_t j = a; j < total; j++) w |= (uint32_t)fp8[j] << (8 * (j - a));
+    }
+    const uint32_t sh = (uint32_t)(byte & 3) * 8u;
+    if constexpr (SPS == 2) {
+        return (((w >> (sh + 3)) & 0xFu) << 4) | ((w >> (sh + 11)) & 0xFu);
+    } else {
+        return (w >> (sh + 3)) & 0xFu;
+    }
+}
+
+// enc_tab[s] = freq | start << 16; next[start + rank] = L + slot.
+template <int SPS>
+__global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
+    const uint8_t* __restrict__ fp8, int64_t K, int64_t N, const uint32_t* __restrict__ enc_tab,
+    const uint16_t* __restrict__ next, int log2L, uint16_t* __restrict__ chunks,
+    uint16_t* __restrict__ states, int* __restrict__ status) {
+    constexpr int NSYM = SPS == 2 ? 256 : 16;
+    __shared__ uint32_t tab[NSYM];
+    __shared__ uint16_t nx[1 << TANS_PAIR_LOG2L];
+    const uint32_t L = 1u << log2L;
+    for (int i = threadIdx.x; i < NSYM; i += blockDim.x) tab[i] = enc_tab[i];
+    for (uint32_t i = threadIdx.x; i < L; i += blockDim.x) nx[i] = next[i];
+    __syncthreads();
+    const int64_t k = (int64_t)blockIdx.x * kEncBlock + threadIdx.x;
+    if (k >= K) return;
+    const int64_t S = N / SPS;
+    const int64_t row = k * N;
+    uint32_t x = L;
+    bool bad = false;
+    for (int64_t i = S - 1; i >= 0; i--) {
+        const uint32_t s = symbol_at<SPS>(fp8, row + i * SPS, K * N);
+        const uint32_t e = tab[s];
+        uint32_t f = e & 0xFFFFu;
+        if (f == 0) {   // not encodable: flag it and keep every index in range
+            bad = true;
+            f = 1;
+        }
+        int nb = (31 - __builtin_clz(x)) - (31 - __builtin_clz(f));
+        if ((x >> nb) < f) nb--;
+        chunks[i * K + k] = (uint16_t)((x & ((1u << nb) - 1u)) | ((uint32_t)nb << 12));
+        uint32_t idx = (e >> 16) + (x >> nb) - f;
+        idx = idx < L ? idx : L - 1u;
+        x = nx[idx];
+    }
+    states[k] = (uint16_t)x;
+    if (bad) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
+}
+
+// The refill schedule, replayed by both forward passes: before step 2q each
+// active lane holding fewer than 24 bits takes the next word (+32 bits), then
+// steps 2q and 2q + 1 consume their nb bits.
+__global__ __launch_bounds__(kEncBlock) void enc_pack_kernel(
+    const uint16_t* __restrict__ chunks, int64_t K, int64_t S, int64_t max_words,
+    uint32_t* __restrict__ words, uint32_t* __restrict__ nwords, uint32_t* __restrict__ glen) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) + threadIdx.x / kLanes;
+    const int64_t G = (K + kLanes - 1) / kLanes;
+    if (g >= G) return;   // wave-uniform
+    const int64_t k = g * kLanes + lane;
+    const bool active = k < K;
+    const int64_t kk = active ? k : K - 1;
+    uint64_t acc = 0;
+    int n = 0;
+    uint32_t nw = 0, taken = 0;
+    int cnt = 0;
+    const int64_t n_checks = (S + 1) / 2;
+    for (int64_t q = 0; q < n_checks; q++) {
+        if (cnt < kRefillBelow) {
+            taken++;
+            cnt += 32;
+        }
+        #pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int64_t t = 2 * q + h;
+            if (t >= S) break;
+            const uint32_t c = chunks[t * K + kk];
+            const int nb = (int)(c >> 12);
+            cnt -= nb;
+            acc |= (uint64_t)(c & 0xFFFu) << n;
+            n += nb;
+            if (n >= 32) {
+                if (active && nw < max_words) words[(int64_t)nw * K + k] = (uint32_t)acc;
+                nw++;
+                acc >>= 32;
+                n -= 32;
+            }
+        }
+    }
+    if (n > 0) {
+        if (active && nw < max_words) words[(int64_t)nw * K + k] = (uint32_t)acc;
+        nw++;
+    }
+    if (active) nwords[k] = nw;
+    // group total: the words active lanes take, padded to a multiple of 4
+    uint32_t tot = active ? taken : 0u;
+    #pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m, kLanes);
+    if (lane == 0) glen[g] = (tot + 3u) & ~3u;
+}
+
+// offsets[g] = sum of glen[0..g), offsets[G] = total; one workgroup: each
+// thread sums a contiguous run, then a Hillis-Steele scan over the threads.
+__global__ __launch_bounds__(1024) void enc_scan_kernel(const uint32_t* __restrict__ glen,
+                                                        int64_t G, int64_t* __restrict__ offsets) {
+    __shared__ int64_t part[1024];
+    const int tid = threadIdx.x;
+    const int64_t per = (G + 1023) / 1024;
+    const int64_t b = tid * per;
+    int64_t sum = 0;
+    for (int64_t i = b; i < b + per && i < G; i++) sum += glen[i];
+    part[tid] = sum;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int64_t v = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += v;
+        __syncthreads();
+    }
+    if (tid == 1023) offsets[G] = part[1023];
+    int64_t run = part[tid] - sum;
+    for (int64_t i = b; i < b + per && i < G; i++) {
+        offsets[i] = run;
+        run += glen[i];
+    }
+}
+
+// Zero n words (a kernel rather than hipMemsetAsync, so a caller may
+// capture the encoder in a graph).
+__global__ __launch_bounds__(kEncBlock) void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * kEncBlock + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+__global__ __launch_bounds__(kEncBlock) void enc_interleave_kernel(
+    const uint16_t* __restrict__ chunks, int64_t K, int64_t S, int64_t max_words,
+    const uint32_t* __restrict__ words, const uint32_t* __restrict__ nwords,
+    const int64_t* __restrict__ offsets, uint32_t* __restrict__ comp) {
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) + threadIdx.x / kLanes;
+    const int64_t G = (K + kLanes - 1) / kLanes;
+    if (g >= G) return;   // wave-uniform
+    const int64_t k = g * kLanes + lane;
+    const bool active = k < K;
+    const int64_t kk = active ? k : K - 1;
+    const uint32_t nw = active ? nwords[k] : 0u;
+    const int64_t base = offsets[g];
+    const int64_t end = offsets[g + 1];
+    int64_t handed = 0;
+    uint32_t taken = 0;
+    int cnt = 0;
+    const int64_t n_checks = (S + 1) / 2;
+    for (int64_t q = 0; q < n_checks; q++) {
+        const bool need = active && cnt < kRefillBelow;
+        const uint64_t m = __ballot(need);
+        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (need) {
+            const uint32_t w = (taken < nw && taken < max_words)
+                                   ? words[(int64_t)taken * K + k] : 0u;
+            const int64_t pos = base + handed + rank;
+            if (pos < end) comp[pos] = w;
+            taken++;
+            cnt += 32;
+        }
+        handed += __popcll(m);
+        #pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int64_t t = 2 * q + h;
+            if (t >= S) break;
+            cnt -= (int)(chunks[t * K + kk] >> 12);
+        }
+    }
+    // zero padding up to the 4-word boundary
+    if (base + handed + lane < end) comp[base + handed + lane] = 0u;
+}
+
+// Sign/mantissa tiles: thread (t, k) writes sm[(t K + k) * 8] from bytes
+// [16t, 16t + 16) of lane k (zero past N).
+__global__ __launch_bounds__(kEncBlock) void enc_sm_kernel(const uint8_t* __restrict__ fp8,
+                                                           int64_t K, int64_t N, int64_t n_tiles,
+                                                           uint32_t* __restrict__ sm) {
+    const int64_t i = (int64_t)blockIdx.x * kEncBlock + threadIdx.x;
+    if (i >= n_tiles * K) return;
+    const int64_t t = i / K, k = i % K;
+    const uint8_t* row = fp8 + k * N;
+    uint32_t b[4];
+    if (N % kTile == 0) {   // whole, 16-byte aligned tiles
+        const uint4 v = *reinterpret_cast<const uint4*>(row + t * kTile);
+        b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
+    } else {
+        #pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t v = 0;
+            #pragma unroll
+            for (int y = 0; y < 4; y++) {
+                const int64_t c = t * kTile + 4 * j + y;
+                if (c < N) v |= (uint32_t)row[c] << (8 * y);
+            }
+            b[j] = v;
+        }
+    }
+    const uint32_t m = 0x87878787u;
+    const uint32_t w0 = (b[0] & m) | __builtin_amdgcn_alignbit(b[1] & m, b[1] & m, 28u);
+    const uint32_t w1 = (b[2] & m) | __builtin_amdgcn_alignbit(b[3] & m, b[3] & m, 28u);
+    sm[2 * i] = w0;
+    sm[2 * i + 1] = w1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tans_gpu_encode_workspace(int64_t K, int64_t N, int32_t log2L, int64_t* workspace_bytes) {
+    if (!workspace_bytes || K < 0 || N < 0 || N % 2)
+        return fail(TANS_EINVAL, "gpu_encode: need K >= 0 and even N >= 0");
+    if (log2L != TANS_PAIR_LOG2L && log2L != TANS_NIBBLE_LOG2L)
+        return fail(TANS_EINVAL, "gpu_encode: log2L must be 12 (pair) or 11 (nibble)");
+    const int64_t S = log2L == TANS_PAIR_LOG2L ? N / 2 : N;
+    *workspace_bytes = ws_layout(K, S, log2L).total;
+    return TANS_OK;
+}
+
+int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t* enc_tab,
+                          const uint16_t* enc_next, int32_t log2L, void* workspace,
+                          int64_t workspace_bytes, int64_t* offsets, uint16_t* states, void* sm,
+                          int32_t* status, void* stream) {
+    int64_t need = 0;
+    int rc = tans_gpu_encode_workspace(K, N, log2L, &need);
+    if (rc) return rc;
+    if (K == 0 || N == 0) {
+        if (K == 0 && offsets) {   // offsets = {0}
+            hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kEncBlock), 0, (hipStream_t)stream,
+                               reinterpret_cast<uint32_t*>(offsets), (int64_t)2);
+            return hip_check(hipGetLastError(), "gpu_encode offsets");
+        }
+        return fail(TANS_EINVAL, "gpu_encode: N must be positive when K > 0");
+    }
+    if (!fp8 || !enc_tab || !enc_next || !workspace || !offsets || !states || !sm || !status)
+        return fail(TANS_EINVAL, "gpu_encode: null pointer");
+    if (workspace_bytes < need) return fail(TANS_EINVAL, "gpu_encode: workspace too small");
+    const int sps = log2L == TANS_PAIR_LOG2L ? 2 : 1;
+    const int64_t S = N / sps;
+    const int64_t G = (K + kLanes - 1) / kLanes;
+    const int64_t max_words = (S * log2L + 31) / 32 + 1;
+    const int64_t n_tiles = (N + kTile - 1) / kTile;
+    if (K > INT32_MAX || S > (int64_t(1) << 24) || n_tiles * K / kEncBlock + 1 > INT32_MAX)
+        return fail(TANS_EINVAL, "gpu_encode: tensor too large");
+    const WsLayout l = ws_layout(K, S, log2L);
+    char* ws = static_cast<char*>(workspace);
+    uint16_t* chunks = reinterpret_cast<uint16_t*>(ws + l.chunks);
+    uint32_t* words = reinterpret_cast<uint32_t*>(ws + l.words);
+    uint32_t* nwords = reinterpret_cast<uint32_t*>(ws + l.nwords);
+    uint32_t* glen = reinterpret_cast<uint32_t*>(ws + l.glen);
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned lane_blocks = (unsigned)((K + kEncBlock - 1) / kEncBlock);
+    const unsigned group_blocks = (unsigned)((G + kEncBlock / kLanes - 1) / (kEncBlock / kLanes));
+    if (sps == 2)
+        hipLaunchKernelGGL(enc_backward_kernel<2>, dim3(lane_blocks), dim3(kEncBlock), 0, st,
+                           (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
+                           states, status);
+    else
+        hipLaunchKernelGGL(enc_backward_kernel<1>, dim3(lane_blocks), dim3(kEncBlock), 0, st,
+                           (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
+                           states, status);
+    if ((rc = hip_check(hipGetLastError(), "enc_backward_kernel launch"))) return rc;
+    hipLaunchKernelGGL(enc_pack_kernel, dim3(group_blocks), dim3(kEncBlock), 0, st, chunks, K, S,
+                       max_words, words, nwords, glen);
+    if ((rc = hip_check(hipGetLastError(), "enc_pack_kernel launch"))) return rc;
+    hipLaunchKernelGGL(enc_scan_kernel, dim3(1), dim3(1024), 0, st, glen, G, offsets);
+    if ((rc = hip_check(hipGetLastError(), "enc_scan_kernel launch"))) return rc;
+    hipLaunchKernelGGL(enc_sm_kernel, dim3((unsigned)((n_tiles * K + kEncBlock - 1) / kEncBlock)),
+                       dim3(kEncBlock), 0, st, (const uint8_t*)fp8, K, N, n_tiles,
+                       (uint32_t*)sm);
+    return hip_check(hipGetLastError(), "enc_sm_kernel launch");
+}
+
+int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* workspace,
+                           const int64_t* offsets, void* comp, int64_t comp_bytes, void* stream) {
+    int64_t need = 0;
+    int rc = tans_gpu_encode_workspace(K, N, log2L, &need);
+    if (rc) return rc;
+    if (!workspace || !offsets || !comp) return fail(TANS_EINVAL, "gpu_encode: null pointer");
+    if (comp_bytes < kTailWords * 4 || comp_bytes % 4)
+        return fail(TANS_EINVAL, "gpu_encode: comp must hold the stream words and the 1 KiB tail");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t words_total = comp_bytes / 4 - kTailWords;
+    uint32_t* c32 = static_cast<uint32_t*>(comp);
+    if (K > 0 && N > 0) {
+        const int sps = log2L == TANS_PAIR_LOG2L ? 2 : 1;
+        const int64_t S = N / sps;
+        const int64_t G = (K + kLanes - 1) / kLanes;
+        const int64_t max_words = (S * log2L + 31) / 32 + 1;
+        const WsLayout l = ws_layout(K, S, log2L);
+        const char* ws = static_cast<const char*>(workspace);
+        hipLaunchKernelGGL(enc_interleave_kernel,
+                           dim3((unsigned)((G + kEncBlock / kLanes - 1) / (kEncBlock / kLanes))),
+                           dim3(kEncBlock), 0, st, reinterpret_cast<const uint16_t*>(ws + l.chunks),
+                           K, S, max_words, reinterpret_cast<const uint32_t*>(ws + l.words),
+                           reinterpret_cast<const uint32_t*>(ws + l.nwords), offsets, c32);
+        if ((rc = hip_check(hipGetLastError(), "enc_interleave_kernel launch"))) return rc;
+    }
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((kTailWords + kEncBlock - 1) / kEncBlock)),
+                       dim3(kEncBlock), 0, st, c32 + words_total, kTailWords);
+    return hip_check(hipGetLastError(), "gpu_encode tail");
+}
+
+}  // extern "C"

@@ -26,6 +26,10 @@ EXPORTS = (
     "tans_decode",
     "tans_fp8_gemm_fused",
     "tans_fp8_gemm_raw",
+    "tans_build_encode_table",
+    "tans_gpu_encode_workspace",
+    "tans_gpu_encode_begin",
+    "tans_gpu_encode_finish",
 )
 
 TANS_LANES = 64
@@ -63,6 +67,10 @@ for _name, _args in {
     "tans_fp8_gemm_fused": [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _I64,
                             ctypes.c_float, _P, _I64, _P, _P],
     "tans_fp8_gemm_raw": [_P, _I64, _I64, _P, _I64, ctypes.c_float, _P, _P],
+    "tans_build_encode_table": [_P, _P, _I32, _I32, _P, _P],
+    "tans_gpu_encode_workspace": [_I64, _I64, _I32, ctypes.POINTER(_I64)],
+    "tans_gpu_encode_begin": [_P, _I64, _I64, _P, _P, _I32, _P, _I64, _P, _P, _P, _P, _P],
+    "tans_gpu_encode_finish": [_I64, _I64, _I32, _P, _P, _P, _I64, _P],
 }.items():
     getattr(lib, _name).restype = ctypes.c_int
     getattr(lib, _name).argtypes = _args

@@ -263,3 +263,66 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
     comp, states, offsets, partial, sm, freqs, spread = encode(slab, exp_freqs, alphabet=alphabet)
     return TansMatrix(comp, states, offsets, partial, sm, freqs, spread, rows=R, cols=C,
                       segments=S, seg_cols=Nc, alphabet=alphabet)
+
+
+# ---------------------------------------------------------------------------
+# GPU encoder (the same bytes as encode(), from FP8 bytes on the device)
+# ---------------------------------------------------------------------------
+
+def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair"):
+    """encode() on the GPU: FP8 bytes [K, N] (uint8, on a GPU, N even) ->
+    the same 7-tuple with the same bytes, as device tensors (freqs and
+    spread included, ready for gpu_tans_decode).  Reads the stream length
+    back from the device once (the size of the compressed tensor)."""
+    if not (isinstance(fp8_bytes, torch.Tensor) and fp8_bytes.dim() == 2
+            and fp8_bytes.dtype == torch.uint8):
+        raise ValueError("fp8_bytes must be a 2-D uint8 tensor [K, N]")
+    if not fp8_bytes.is_cuda:
+        raise ValueError("encode_gpu needs a GPU tensor; use encode() for CPU tensors")
+    if alphabet not in ALPHABETS:
+        raise ValueError(f"alphabet must be one of {sorted(ALPHABETS)}")
+    if tile not in (0, TILE_PAIRS):
+        raise ValueError(f"tile must be 0 or {TILE_PAIRS}")
+    K, N = fp8_bytes.shape
+    if N % 2:
+        raise ValueError("N must be even")
+    if isinstance(exp_freqs, torch.Tensor):
+        exp_freqs = exp_freqs.detach().cpu().float().numpy()
+    nsym, L, _ = ALPHABETS[alphabet]
+    log2L = L.bit_length() - 1
+    freqs = symbol_freqs(exp_freqs, alphabet)
+    spread = build_spread(freqs)
+    enc_tab = np.empty(nsym, dtype=np.uint32)
+    enc_next = np.empty(L, dtype=np.uint16)
+    check(lib.tans_build_encode_table(ctypes.c_void_p(spread.ctypes.data),
+                                      ctypes.c_void_p(freqs.ctypes.data), nsym, log2L,
+                                      ctypes.c_void_p(enc_tab.ctypes.data),
+                                      ctypes.c_void_p(enc_next.ctypes.data)),
+          "encode_gpu")
+    dev = fp8_bytes.device
+    x = fp8_bytes.contiguous()
+    G = -(-K // TANS_LANES)
+    with torch.cuda.device(dev):
+        ws_bytes = ctypes.c_int64()
+        check(lib.tans_gpu_encode_workspace(K, N, log2L, ctypes.byref(ws_bytes)), "encode_gpu")
+        ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=dev)
+        offsets = torch.empty(G + 1, dtype=torch.int64, device=dev)
+        states = torch.empty(K, dtype=torch.uint16, device=dev)
+        sm = torch.empty(((N + 15) // 16, K, 8), dtype=torch.uint8, device=dev)
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+        tab_d = torch.from_numpy(enc_tab.view(np.int32)).to(dev)
+        next_d = torch.from_numpy(enc_next.view(np.int16)).to(dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        check(lib.tans_gpu_encode_begin(x.data_ptr(), K, N, tab_d.data_ptr(), next_d.data_ptr(),
+                                        log2L, ws.data_ptr(), ws.numel(), offsets.data_ptr(),
+                                        states.data_ptr(), sm.data_ptr(), status.data_ptr(),
+                                        stream), "encode_gpu")
+        total, bad = (int(v) for v in torch.stack([offsets[G], status[0].to(torch.int64)]).tolist())
+        if bad:
+            raise RuntimeError("encode_gpu: data holds a symbol whose frequency is 0")
+        comp = torch.empty((total + 256) * 4, dtype=torch.uint8, device=dev)
+        check(lib.tans_gpu_encode_finish(K, N, log2L, ws.data_ptr(), offsets.data_ptr(),
+                                         comp.data_ptr(), comp.numel(), stream), "encode_gpu")
+    partial = torch.empty(0, dtype=torch.uint8, device=dev)
+    return (comp, states, offsets, partial, sm, torch.from_numpy(freqs).to(dev),
+            torch.from_numpy(spread).to(dev))

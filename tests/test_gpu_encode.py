@@ -1,0 +1,78 @@
+"""GPU encoder (tans_codec.encode_gpu) against the CPU encoder, byte for byte:
+compressed words, offsets, states and sign/mantissa tiles, at the reference's
+test shapes (test_gpu_decode_tans.py:69-74, seed 42, Qwen3 histogram) and
+ragged ones, then GPU encode -> GPU decode round trips on config data."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+ALPHABETS = ["pair", "nibble"]
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def R():
+    import rans_vectoradd
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return rans_vectoradd
+
+
+def _compare(T, fp8, hist, alphabet):
+    cpu = T.encode(fp8, hist, alphabet=alphabet)
+    gpu = T.encode_gpu(fp8.cuda(), hist, alphabet=alphabet)
+    names = ("comp", "states", "offsets", "partial", "sm", "freqs", "spread")
+    for name, c, g in zip(names, cpu, gpu):
+        assert g.is_cuda, name
+        assert torch.equal(c, g.cpu()), f"{name} differs"
+    return gpu
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("K,N", [(128, 128), (1024, 128), (10000, 128), (100000, 128),
+                                 (64, 2), (65, 18), (200, 130), (3, 1000), (1, 16),
+                                 (127, 4096), (130, 30), (4096, 14)])
+def test_gpu_encode_matches_cpu(R, alphabet, K, N):
+    from rans_vectoradd import tans_codec as T
+    _say(f"case: encode_gpu K={K} N={N} {alphabet}")
+    torch.manual_seed(42)
+    fp8 = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
+    _compare(T, fp8, torch.tensor(R.QWEN3_14B_FP8_EXP), alphabet)
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("dist", ["gaussian", "laplace"])
+def test_gpu_encode_config_data_roundtrip(R, alphabet, dist):
+    """2^24 config data (own histogram, 1024 per lane): GPU encode == CPU
+    encode, and GPU decode of the GPU encoding == the input."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: encode_gpu {dist} 2^24 {alphabet}")
+    n, N = 1 << 24, 1024
+    gen = D.gaussian_fp8_bytes if dist == "gaussian" else D.laplace_fp8_bytes
+    q, _ = gen(n, seed=9)
+    fp8 = q.reshape(n // N, N)
+    comp, st, off, part, sm, fr, sp = _compare(T, fp8, D.exp_histogram(q), alphabet)
+    dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
+    assert torch.equal(dec.cpu(), fp8.t())
+
+
+def test_gpu_encode_edge_cases(R):
+    from rans_vectoradd import tans_codec as T
+    exp = torch.tensor(R.QWEN3_14B_FP8_EXP)
+    comp, st, off, part, sm, fr, sp = T.encode_gpu(torch.zeros((0, 16), dtype=torch.uint8).cuda(), exp)
+    assert st.numel() == 0 and off.cpu().tolist() == [0] and comp.numel() == 1024
+    assert int(comp.sum()) == 0
+    # a symbol whose frequency is 0 is reported, as by the CPU encoder
+    hist = torch.zeros(16)
+    hist[7] = 1.0
+    fp8 = torch.full((64, 32), 7 << 3, dtype=torch.uint8)
+    fp8[5, 3] = 9 << 3
+    with pytest.raises(RuntimeError, match="frequency is 0"):
+        T.encode_gpu(fp8.cuda(), hist, alphabet="nibble")
+    with pytest.raises(ValueError):
+        T.encode_gpu(torch.zeros((4, 16), dtype=torch.uint8), exp)       # CPU tensor
+    with pytest.raises(ValueError):
+        T.encode_gpu(torch.zeros((4, 15), dtype=torch.uint8).cuda(), exp)
