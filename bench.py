@@ -135,20 +135,45 @@ def make_inputs(seed: int):
 
 
 def encode_pair(qa_d, qb_d, hist, lane: int, alphabet: str):
-    """Encode a and b on the CPU; returns the device argument list of
-    fp8_vecadd_fused_tans, the compressed byte count and the encode time."""
+    """Encode a and b with the GPU encoder (the same bytes as the CPU one);
+    returns the device argument list of fp8_vecadd_fused_tans, the
+    compressed byte count and the encode time of both."""
+    import torch
     from rans_vectoradd import tans_codec as T
 
     K = N_ELEMS // lane
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ea = T.encode(qa_d.cpu().reshape(K, lane), hist, tile=8, alphabet=alphabet)
-    eb = T.encode(qb_d.cpu().reshape(K, lane), hist, tile=8, alphabet=alphabet)
+    ea = T.encode_gpu(qa_d.reshape(K, lane), hist, tile=8, alphabet=alphabet)
+    eb = T.encode_gpu(qb_d.reshape(K, lane), hist, tile=8, alphabet=alphabet)
+    torch.cuda.synchronize()
     t_enc = time.perf_counter() - t0
-    tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy())
+    tbl = T.build_decode_table(ea[6].cpu().numpy(), ea[5].cpu().numpy()).cuda()
     order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
-    args = [x.cuda() for x in (*[ea[i] for i in order], *[eb[i] for i in order], tbl)]
+    args = [*[ea[i] for i in order], *[eb[i] for i in order], tbl]
     in_bytes = T.compressed_bytes(*ea[:5]) + T.compressed_bytes(*eb[:5])
     return args, in_bytes, t_enc
+
+
+def gpu_encode_rate(q_d, hist, lane: int, alphabet: str, reps: int = 5) -> dict:
+    """Wall time of encode_gpu on one 2^29-element tensor (best of reps,
+    after a first call), with the CPU encoder's rate beside it in the
+    cpu_baseline entry."""
+    import torch
+    from rans_vectoradd import tans_codec as T
+
+    K = q_d.numel() // lane
+    x = q_d.reshape(K, lane)
+    T.encode_gpu(x, hist, alphabet=alphabet)
+    best = 1e9
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        T.encode_gpu(x, hist, alphabet=alphabet)
+        torch.cuda.synchronize()
+        best = min(best, time.perf_counter() - t0)
+    return {"elements": q_d.numel(), "alphabet": alphabet, "seconds": best,
+            "gbs": q_d.numel() / best / 1e9}
 
 
 def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps: int,
@@ -192,12 +217,12 @@ def run_decode_config(dist: str, alphabet: str, seed: int, steps: int, warmup: i
     gen = D.gaussian_fp8_bytes if dist == "gaussian" else D.laplace_fp8_bytes
     q, _ = gen(n, seed=seed, device="cuda")
     hist = D.exp_histogram(q).cpu()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    e = T.encode(q.cpu().reshape(K, lane), hist, alphabet=alphabet)
+    comp, st, off, part, sm, fr, sp = T.encode_gpu(q.reshape(K, lane), hist, alphabet=alphabet)
+    torch.cuda.synchronize()
     t_enc = time.perf_counter() - t0
-    in_bytes = T.compressed_bytes(*e[:5])
-    comp, st, off, part, sm, fr, sp = [x.cuda() for x in e]
-    del e
+    in_bytes = T.compressed_bytes(comp, st, off, part, sm)
     fn = lambda: R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, lane)   # noqa: E731
     out = fn()
     exact = bool(torch.equal(out, q.view(K, lane).t()))
@@ -445,10 +470,9 @@ def profile_only(args) -> None:
         from rans_vectoradd import data as D
         K = DECODE_ELEMS // HEADLINE_LANE
         q, _ = D.gaussian_fp8_bytes(DECODE_ELEMS, seed=args.seed, device="cuda")
-        e = T.encode(q.cpu().reshape(K, HEADLINE_LANE), D.exp_histogram(q).cpu(),
-                     alphabet=args.alphabet)
+        d = T.encode_gpu(q.reshape(K, HEADLINE_LANE), D.exp_histogram(q).cpu(),
+                         alphabet=args.alphabet)
         del q
-        d = [x.cuda() for x in e]
         fn = lambda: R.gpu_tans_decode(d[0], d[2], d[1], d[3], d[4], d[6], d[5], HEADLINE_LANE)  # noqa
     else:
         qa, qb, hist = make_inputs(args.seed)
@@ -539,6 +563,10 @@ def main() -> None:
                                      "exact_vs_raw")}
                   | {"x_raw": raw_kernel / r["kernel_ms"]} for r in results],
     }
+    log("gpu encoder")
+    line["gpu_encode"] = gpu_encode_rate(qa, hist, HEADLINE_LANE, "pair")
+    log(f"  encode_gpu 2^29 elements: {line['gpu_encode']['seconds'] * 1e3:.2f} ms  "
+        f"{line['gpu_encode']['gbs']:.1f} GB/s")
     del raw_out, qa, qb
     torch.cuda.empty_cache()
     if not args.no_decode:
