@@ -1,0 +1,99 @@
+"""On-disk container for tANS-coded FP8 tensors (no counterpart in the
+reference, which encodes in memory each run).
+
+A container is one safetensors file, so it loads without executing anything
+from the file.  For each encoded entry ``name`` it holds the tensors
+``name.comp`` (uint8), ``name.states`` (uint16), ``name.offsets`` (int64),
+``name.sm`` (uint8 tiles), ``name.freqs`` and ``name.spread`` (int32), and
+the metadata key ``tans:name`` with a JSON description:
+
+* ``{"kind": "lanes", "K", "N", "alphabet"}`` for a TansTensor (K lanes of N
+  elements, the layout of gpu_tans_decode and fp8_vecadd_fused_tans);
+* ``{"kind": "matrix", "rows", "cols", "segments", "seg_cols", "alphabet"}``
+  for a TansMatrix (the layout of fp8_gemm_fused_tans).
+
+Plain tensors (scales, unencoded weights) are stored under their own names;
+``tans_format`` in the metadata names the layout version.
+"""
+from __future__ import annotations
+
+import json
+
+import torch
+
+from .tans_codec import TansMatrix, TansTensor
+
+FORMAT = "tans-wave64-v1"
+_PARTS = ("comp", "states", "offsets", "sm", "freqs", "spread")
+
+
+def save(path: str, entries: dict, metadata: dict | None = None) -> None:
+    """Write ``entries`` (name -> TansTensor, TansMatrix or torch.Tensor) to
+    ``path``.  Tensors are copied to the CPU; ``metadata`` adds string keys."""
+    from safetensors.torch import save_file
+
+    tensors: dict[str, torch.Tensor] = {}
+    meta = {"tans_format": FORMAT}
+    for k, v in (metadata or {}).items():
+        if k.startswith("tans"):
+            raise ValueError("metadata keys starting with 'tans' are reserved")
+        meta[str(k)] = str(v)
+    for name, e in entries.items():
+        if "." in name and isinstance(e, (TansTensor, TansMatrix)):
+            raise ValueError(f"encoded entry names may not contain '.': {name}")
+        if isinstance(e, TansTensor):
+            desc = {"kind": "lanes", "K": e.K, "N": e.N, "alphabet": e.alphabet}
+        elif isinstance(e, TansMatrix):
+            desc = {"kind": "matrix", "rows": e.rows, "cols": e.cols, "segments": e.segments,
+                    "seg_cols": e.seg_cols, "alphabet": e.alphabet}
+        elif isinstance(e, torch.Tensor):
+            tensors[name] = e.detach().cpu().contiguous()
+            continue
+        else:
+            raise TypeError(f"{name}: cannot store {type(e).__name__}")
+        for part in _PARTS:
+            tensors[f"{name}.{part}"] = getattr(e, part).detach().cpu().contiguous()
+        meta[f"tans:{name}"] = json.dumps(desc)
+    save_file(tensors, path, metadata=meta)
+
+
+def load(path: str, device="cpu") -> dict:
+    """Read a container: name -> TansTensor / TansMatrix / torch.Tensor, with
+    every tensor on ``device``."""
+    from safetensors import safe_open
+
+    out: dict = {}
+    with safe_open(path, framework="pt", device="cpu") as f:
+        meta = f.metadata() or {}
+        if meta.get("tans_format") != FORMAT:
+            raise ValueError(f"{path}: not a {FORMAT} container")
+        keys = set(f.keys())
+        encoded = {k[len("tans:"):]: json.loads(v) for k, v in meta.items() if k.startswith("tans:")}
+        for name, desc in encoded.items():
+            parts = {p: f.get_tensor(f"{name}.{p}").to(device) for p in _PARTS}
+            keys -= {f"{name}.{p}" for p in _PARTS}
+            partial = torch.empty(0, dtype=torch.uint8, device=device)
+            if desc["kind"] == "lanes":
+                out[name] = TansTensor(parts["comp"], parts["states"], parts["offsets"], partial,
+                                       parts["sm"], parts["freqs"], parts["spread"],
+                                       K=int(desc["K"]), N=int(desc["N"]),
+                                       alphabet=desc["alphabet"])
+            elif desc["kind"] == "matrix":
+                out[name] = TansMatrix(parts["comp"], parts["states"], parts["offsets"], partial,
+                                       parts["sm"], parts["freqs"], parts["spread"],
+                                       rows=int(desc["rows"]), cols=int(desc["cols"]),
+                                       segments=int(desc["segments"]),
+                                       seg_cols=int(desc["seg_cols"]), alphabet=desc["alphabet"])
+            else:
+                raise ValueError(f"{path}: entry {name} has unknown kind {desc['kind']}")
+        for k in sorted(keys):
+            out[k] = f.get_tensor(k).to(device)
+    return out
+
+
+def metadata(path: str) -> dict:
+    """The user metadata of a container (without the reserved tans keys)."""
+    from safetensors import safe_open
+
+    with safe_open(path, framework="pt", device="cpu") as f:
+        return {k: v for k, v in (f.metadata() or {}).items() if not k.startswith("tans")}

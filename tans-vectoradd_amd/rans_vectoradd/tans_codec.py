@@ -326,3 +326,39 @@ def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: s
     partial = torch.empty(0, dtype=torch.uint8, device=dev)
     return (comp, states, offsets, partial, sm, torch.from_numpy(freqs).to(dev),
             torch.from_numpy(spread).to(dev))
+
+
+@dataclasses.dataclass
+class TansTensor:
+    """A tANS-coded FP8 tensor in the lane layout: K lanes of N elements,
+    the encode() 7-tuple plus its shape and alphabet (what a caller keeps to
+    decode or add it later; stored by rans_vectoradd.container)."""
+    comp: torch.Tensor
+    states: torch.Tensor
+    offsets: torch.Tensor
+    partial: torch.Tensor
+    sm: torch.Tensor
+    freqs: torch.Tensor
+    spread: torch.Tensor
+    K: int
+    N: int
+    alphabet: str
+
+    @classmethod
+    def from_tuple(cls, enc, K: int, N: int, alphabet: str = "pair") -> "TansTensor":
+        return cls(*enc, K=K, N=N, alphabet=alphabet)
+
+    def as_tuple(self):
+        return (self.comp, self.states, self.offsets, self.partial, self.sm, self.freqs,
+                self.spread)
+
+    def to(self, device) -> "TansTensor":
+        moved = {f.name: getattr(self, f.name).to(device)
+                 for f in dataclasses.fields(self) if isinstance(getattr(self, f.name), torch.Tensor)}
+        return dataclasses.replace(self, **moved)
+
+    def decode_table(self) -> torch.Tensor:
+        return build_decode_table(self.spread.cpu().numpy(), self.freqs.cpu().numpy())
+
+    def compressed_bytes(self) -> int:
+        return compressed_bytes(self.comp, self.states, self.offsets, self.partial, self.sm)

@@ -1,0 +1,121 @@
+"""The on-disk container and checkpoint ingestion (CPU): safetensors round
+trips, histograms against numpy, and encoded entries decoded back to the
+original bytes by the oracle's independent decoder."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+LOG2L = {"pair": (12, 2), "nibble": (11, 1)}
+
+
+def _decode_lanes(e):
+    log2L, sps = LOG2L[e.alphabet]
+    return O.w64_decode(e.comp.numpy(), e.offsets.numpy(), e.states.numpy(), e.sm.numpy(),
+                        e.spread.numpy(), e.freqs.numpy(), log2L, sps, e.K, e.N)
+
+
+def _decode_matrix(m):
+    log2L, sps = LOG2L[m.alphabet]
+    Rp = -(-m.rows // 64) * 64
+    dec = O.w64_decode(m.comp.numpy(), m.offsets.numpy(), m.states.numpy(), m.sm.numpy(),
+                       m.spread.numpy(), m.freqs.numpy(), log2L, sps, m.segments * Rp, m.seg_cols)
+    slab = dec.reshape(m.segments, Rp, m.seg_cols).transpose(1, 0, 2).reshape(Rp, -1)
+    return slab[:m.rows, :m.cols]
+
+
+def test_container_roundtrip(tmp_path):
+    from rans_vectoradd import container, data as D, tans_codec as T
+    q, _ = D.gaussian_fp8_bytes(64 * 96, seed=4)
+    lanes = T.TansTensor.from_tuple(T.encode(q.reshape(64, 96), D.exp_histogram(q)), 64, 96, "pair")
+    w, _ = D.laplace_fp8_bytes(100 * 70, seed=5)
+    mat = T.encode_matrix(w.reshape(100, 70), D.exp_histogram(w), alphabet="nibble")
+    scale = torch.tensor([0.125], dtype=torch.float32)
+    path = os.path.join(tmp_path, "c.safetensors")
+    container.save(path, {"a": lanes, "w": mat, "w_scale": scale}, metadata={"note": "x"})
+    got = container.load(path)
+    assert set(got) == {"a", "w", "w_scale"}
+    assert container.metadata(path) == {"note": "x"}
+    for name, ref in (("a", lanes), ("w", mat)):
+        for part in ("comp", "states", "offsets", "sm", "freqs", "spread"):
+            assert torch.equal(getattr(got[name], part), getattr(ref, part)), (name, part)
+    assert (got["a"].K, got["a"].N, got["a"].alphabet) == (64, 96, "pair")
+    assert (got["w"].rows, got["w"].cols, got["w"].segments, got["w"].seg_cols) == \
+        (mat.rows, mat.cols, mat.segments, mat.seg_cols)
+    assert torch.equal(got["w_scale"], scale)
+    assert np.array_equal(_decode_lanes(got["a"]), q.reshape(64, 96).numpy())
+    assert np.array_equal(_decode_matrix(got["w"]), w.reshape(100, 70).numpy())
+
+
+def test_container_rejects_other_files(tmp_path):
+    from safetensors.torch import save_file
+    from rans_vectoradd import container
+    path = os.path.join(tmp_path, "plain.safetensors")
+    save_file({"x": torch.zeros(2)}, path)
+    with pytest.raises(ValueError):
+        container.load(path)
+    with pytest.raises(ValueError):
+        container.save(path, {"x": torch.zeros(2)}, metadata={"tans_format": "y"})
+
+
+def _checkpoint(path):
+    from safetensors.torch import save_file
+    from rans_vectoradd import data as D
+    w1, s1 = D.gaussian_fp8_bytes(192 * 160, seed=11)
+    w2, s2 = D.laplace_fp8_bytes(4096, seed=12)
+    tensors = {
+        "layer0_up": w1.reshape(192, 160).view(torch.float8_e4m3fn),
+        "layer0_up_scale": torch.tensor([s1], dtype=torch.float32),
+        "layer0_vec": w2.view(torch.float8_e4m3fn),
+        "layer0_bias": torch.randn(160, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16),
+    }
+    save_file(tensors, path)
+    return tensors
+
+
+def test_scan_histograms_match_numpy(tmp_path):
+    from rans_vectoradd import ingest
+    src = os.path.join(tmp_path, "ckpt.safetensors")
+    t = _checkpoint(src)
+    hists = ingest.scan(src)
+    assert set(hists) == {"layer0_up", "layer0_vec"}
+    for name, h in hists.items():
+        b = t[name].view(torch.uint8).numpy().reshape(-1)
+        assert np.array_equal(h, np.bincount((b >> 3) & 15, minlength=16).astype(np.float64))
+    slabs = ingest.scan(src, per="slab", rows_per_slab=64)["layer0_up"]
+    assert slabs.shape == (3, 16)
+    assert np.array_equal(slabs.sum(axis=0), hists["layer0_up"])
+    b = t["layer0_up"].view(torch.uint8).numpy()[64:128].reshape(-1)
+    assert np.array_equal(slabs[1], np.bincount((b >> 3) & 15, minlength=16))
+    agg = ingest.aggregate(hists)
+    assert abs(agg.sum() - 1.0) < 1e-12
+    assert np.allclose(agg, (hists["layer0_up"] + hists["layer0_vec"]) /
+                       (hists["layer0_up"].sum() + hists["layer0_vec"].sum()))
+
+
+@pytest.mark.parametrize("table", ["tensor", "global"])
+def test_encode_checkpoint_decodes_back(tmp_path, table):
+    from rans_vectoradd import container, ingest
+    src = os.path.join(tmp_path, "ckpt.safetensors")
+    dst = os.path.join(tmp_path, "ckpt.tans.safetensors")
+    t = _checkpoint(src)
+    report = ingest.encode_checkpoint(src, dst, table=table, lane_elems=256)
+    assert report["layer0_up"]["kind"] == "matrix" and report["layer0_vec"]["kind"] == "lanes"
+    for r in report.values():
+        assert 4.0 < r["bits_per_byte"] < 12.0   # tiny tensors: per-lane states dominate
+    got = container.load(dst)
+    up = got["layer0_up"]
+    assert np.array_equal(_decode_matrix(up), t["layer0_up"].view(torch.uint8).numpy())
+    vec = got["layer0_vec"]
+    assert (vec.K, vec.N) == (16, 256)
+    assert np.array_equal(_decode_lanes(vec).reshape(-1), t["layer0_vec"].view(torch.uint8).numpy())
+    assert torch.equal(got["layer0_bias"], t["layer0_bias"])
+    assert torch.equal(got["layer0_up_scale"], t["layer0_up_scale"])
+    shapes = json.loads(container.metadata(dst)["shapes"])
+    assert shapes["layer0_up"] == {"shape": [192, 160], "dtype": "float8_e4m3fn"}
+    if table == "global":   # one table for both tensors
+        assert torch.equal(up.freqs, vec.freqs)

@@ -76,3 +76,30 @@ def test_gpu_encode_edge_cases(R):
         T.encode_gpu(torch.zeros((4, 16), dtype=torch.uint8), exp)       # CPU tensor
     with pytest.raises(ValueError):
         T.encode_gpu(torch.zeros((4, 15), dtype=torch.uint8).cuda(), exp)
+
+
+def test_checkpoint_container_on_gpu(R, tmp_path):
+    """A checkpoint encoded with the GPU encoder into a container, loaded on
+    the GPU: the lane tensor decodes to its bytes and the matrix gives the
+    same product as the raw FP8 kernel."""
+    import os
+    from safetensors.torch import save_file
+    from rans_vectoradd import container, data as D, ingest
+    _say("case: checkpoint -> container -> GPU")
+    w, scale = D.gaussian_fp8_bytes(1024 * 512, seed=21)
+    v, _ = D.laplace_fp8_bytes(1 << 16, seed=22)
+    src = os.path.join(tmp_path, "ckpt.safetensors")
+    dst = os.path.join(tmp_path, "ckpt.tans.safetensors")
+    save_file({"w": w.reshape(1024, 512).view(torch.float8_e4m3fn),
+               "v": v.view(torch.float8_e4m3fn)}, src)
+    ingest.encode_checkpoint(src, dst, device="cuda")
+    got = container.load(dst, device="cuda")
+    vec = got["v"]
+    dec = R.gpu_tans_decode(vec.comp, vec.offsets, vec.states, vec.partial, vec.sm, vec.spread,
+                            vec.freqs, vec.N)
+    assert torch.equal(dec.t().reshape(-1).cpu(), v)
+    m = got["w"]
+    x = torch.randn(3, 512, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).cuda()
+    y = R.fp8_gemm_fused_tans(m, m.decode_table().cuda(), x, scale).float()
+    y_raw = R.fp8_gemm_raw(w.reshape(1024, 512).cuda(), x, scale).float()
+    assert bool(((y - y_raw).abs() <= 2.0 ** -7 * y_raw.abs() + 1e-6).all())
