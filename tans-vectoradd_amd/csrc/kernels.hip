@@ -1,15 +1,20 @@
-// gfx950 kernels of the tANS FP8 library and their C-ABI launchers.
+// gfx950 kernels of the tANS FP8 library and their C-ABI launchers (the GPU
+// encoder is in encode.hip).
 //
 // Kernels (the data format is described in include/tans_amd.h):
-//   fp8_copy_kernel        16-byte streaming copy, the HBM ceiling
-//                          (role of csrc/fp8_memcpy.cu:30-41)
-//   fp8_add_kernel         uncompressed FP8 add (csrc/vecadd.cu:41-73)
-//   table_kernel           decode table from device spread/freqs
-//                          (csrc/tans_decode.cu:23-59 without the host trip)
-//   fused_add_kernel<SPS>  decode two encodings + FP8 add
-//                          (csrc/vecadd.cu:156-243)
-//   decode_kernel<SPS>     decode to FP8 bytes [N, K]
-//                          (csrc/tans_decode.cu:125-155)
+//   fp8_copy_kernel          16-byte streaming copy, the HBM ceiling
+//                            (role of csrc/fp8_memcpy.cu:30-41)
+//   fp8_add_kernel           uncompressed FP8 add (csrc/vecadd.cu:41-73)
+//   table_kernel             decode table from device spread/freqs
+//                            (csrc/tans_decode.cu:23-59 without the host trip)
+//   fused_add_kernel<SPS,G>  decode two encodings + FP8 add
+//                            (csrc/vecadd.cu:156-243)
+//   decode_kernel<SPS>       decode to FP8 bytes [N, K]
+//                            (csrc/tans_decode.cu:125-155)
+//   gemm_fused_kernel<SPS,B> decode W + skinny GEMM partial sums (no
+//                            counterpart in the reference), with
+//                            gemm_finalize_kernel and the uncompressed
+//                            baseline gemm_raw_kernel<B>
 //
 // Decoder design.  One wave64 decodes one 64-lane group; each lane owns one
 // tANS state.  The decode table lives in LDS as 8-byte entries addressed by
@@ -21,16 +26,16 @@
 // Before every second step, each lane holding fewer than 24 unread bits
 // takes the next word of the group's stream: the ballot of those lanes, an
 // mbcnt for each lane's rank and one ds_read_b32 from the wave's LDS ring.
-// The ring holds kSlots segments of 128 words (one 8-byte load per lane)
+// The ring holds kSlots segments of 256 words (one 16-byte load per lane)
 // plus a 64-word mirror of its first words, so a wave's 64 consecutive reads
-// never wrap.  Segments are fetched by an unconditional per-stage load
-// whose address (the next segment, or a cache-hot idle address when the ring
-// is full or the stream is done) is chosen by scalar code; the data is
-// written into the ring kDelay stages later.  A stage is two refill checks,
-// so at most 128 words are handed out per stage, and kSlots = kDelay + 2
-// guarantees every segment is in the ring before a lane asks for it.  All
-// vector-memory instructions run in a fixed order, so the compiler's
-// wait counts stay exact and no stage waits for a full memory round trip.
+// never wrap.  Each stage issues one segment load per stream through a
+// buffer resource whose bound is the room left in the stream (an idle stage
+// loads with an empty bound, which reads nothing), and writes it into the
+// ring kDelay stages later.  A stage is four refill checks, so at most 256
+// words are handed out per stage, and kSlots = kDelay + 2 guarantees every
+// segment is in the ring before a lane asks for it.  All vector-memory
+// instructions run in a fixed order, so the compiler's wait counts stay
+// exact and no stage waits for a full memory round trip.
 //
 // FP8 bytes are rebuilt four at a time: the table carries each exponent
 // pre-shifted to bits 6:3 of a byte, a v_perm gathers four of them and one
