@@ -419,7 +419,7 @@ def cpu_baseline(seed: int) -> dict:
     a = qa.numpy().reshape(K, lane)
     b = qb.numpy().reshape(K, lane)
     threads = len(os.sched_getaffinity(0))
-    os.environ["OMP_NUM_THREADS"] = str(threads)
+    O.set_threads(threads)
     t0 = time.perf_counter()
     enc = []
     for x in (a, b):
@@ -444,11 +444,48 @@ def cpu_baseline(seed: int) -> dict:
     except OSError:
         pass
     per = t_dec / reps
+    # the same decode+add on one thread (about 3 s)
+    O.set_threads(1)
+    reps1, t1 = 0, 0.0
+    while t1 < 3.0 and reps1 < 200:
+        t0 = time.perf_counter()
+        O.ref_decode_add(enc[0], enc[1], table, lut, K, lane)
+        t1 += time.perf_counter() - t0
+        reps1 += 1
+    O.set_threads(threads)
     return {"value": 3 * n / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"2^25 elements per vector (1024 per stream), decode+add x{reps} "
                       f"(~10 s); encode of both vectors {t_enc:.2f} s",
             "encode_s": t_enc, "encode_gbs": 2 * n / t_enc / 1e9, "decode_add_s": per,
-            "exact": bool(np.array_equal(got, ref)), "cpu_model": cpu}
+            "one_thread": {"value": 3 * n / (t1 / reps1) / 1e9, "decode_add_s": t1 / reps1},
+            "exact": bool(np.array_equal(got, ref)), "cpu_model": cpu,
+            "config0": config0_roundtrip(seed)}
+
+
+def config0_roundtrip(seed: int) -> dict:
+    """BASELINE config 0 on the CPU: 2^24 values N(0, 0.02) scaled to 448,
+    the 16-symbol alphabet with a 2^11-state table from the data's own
+    histogram, encoded by the product's CPU encoder into the lane layout and
+    decoded by the oracle's independent CPU decoder; bits per FP8 byte and
+    bit-exactness."""
+    import numpy as np
+    from oracle import oracle as O
+    from rans_vectoradd import data as D, tans_codec as T
+
+    n, lane = 1 << 24, 1024
+    q, _ = D.gaussian_fp8_bytes(n, seed=seed)
+    x = q.reshape(n // lane, lane)
+    t0 = time.perf_counter()
+    comp, st, off, part, sm, fr, sp = T.encode(x, D.exp_histogram(q), alphabet="nibble")
+    t_enc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    dec = O.w64_decode(comp.numpy(), off.numpy(), st.numpy(), sm.numpy(), sp.numpy(),
+                       fr.numpy(), 11, 1, n // lane, lane)
+    t_dec = time.perf_counter() - t0
+    return {"elements": n, "alphabet": "nibble", "log2L": 11,
+            "bits_per_byte": T.compressed_bytes(comp, st, off, part, sm) * 8 / n,
+            "exact": bool(np.array_equal(dec, x.numpy())), "encode_s": t_enc,
+            "decode_s": t_dec}
 
 
 def profile_only(args) -> None:

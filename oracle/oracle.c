@@ -327,6 +327,10 @@ int ora_ref_decode(const uint8_t* comp8, const int32_t* offsets, const uint16_t*
 
 /* Fused decode + add over two reference-format encodings, tiled output
  * (vecadd.cu:156-243).  `lut` is ora_fp8_add_lut's table. */
+/* Threads used by the OpenMP loops above (the CPU baseline is timed with
+ * all host cores and with one). */
+void ora_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+
 int ora_ref_decode_add(const uint8_t* a_comp8, const int32_t* a_off, const uint16_t* a_st,
                        const uint8_t* a_part, const uint8_t* a_sm,
                        const uint8_t* b_comp8, const int32_t* b_off, const uint16_t* b_st,

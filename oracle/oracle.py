@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
         _lib.ora_ref_encode_write.argtypes = [P, I64, I64, P, I, P, P, P, P, P, P]
         _lib.ora_ref_decode.restype = I
         _lib.ora_ref_decode.argtypes = [P, P, P, P, P, P, I64, I64, P]
+        _lib.ora_set_threads.restype = None
+        _lib.ora_set_threads.argtypes = [I]
         _lib.ora_ref_decode_add.restype = I
         _lib.ora_ref_decode_add.argtypes = [P] * 12 + [I64, I64, P]
         _lib.ora_w64_decode.restype = I
@@ -241,6 +243,11 @@ def ref_decode(comp, offsets, states, partial, sm_kn, table, K: int, N: int) -> 
     args = [np.ascontiguousarray(a) for a in (comp, offsets, states, partial, sm_kn, table)]
     lib().ora_ref_decode(*[_p(a) for a in args], K, N, _p(out))
     return out
+
+
+def set_threads(n: int) -> None:
+    """Threads of the oracle's OpenMP loops."""
+    lib().ora_set_threads(int(n))
 
 
 def ref_decode_add(a_enc, b_enc, table, lut, K: int, N: int) -> np.ndarray:
