@@ -78,3 +78,61 @@ def test_host_table_builder_rejects_inconsistent_input():
     bad[3] = 40
     with pytest.raises(RuntimeError):
         T.build_decode_table(bad, f)                # symbol out of range
+
+
+def test_gemm_and_gpu_encode_entry_points_validate_before_launch():
+    """The decode-GEMM, raw GEMM and GPU encoder entry points reject bad
+    shapes and sizes with TANS_EINVAL before touching the device."""
+    from rans_vectoradd._lib import lib
+    P = ctypes.c_void_p
+    d = P(256)
+    f = ctypes.c_float(1.0)
+    # gemm_fused(comp, bytes, off, st, sm, tbl, log2L, R, C, S, Nc, x, B, scale, ws, ws_bytes, y, stream)
+    ok = (d, 1024, d, d, d, d, 12, 128, 100, 2, 50, d, 1, f, d, 1 << 20, d, None)
+    bad = [
+        dict(i=6, v=10),            # log2L
+        dict(i=12, v=9),            # batch > 8
+        dict(i=12, v=0),            # batch < 1
+        dict(i=10, v=51),           # odd segment width
+        dict(i=10, v=600),          # segment width above 512
+        dict(i=9, v=1),             # S * Nc < C
+        dict(i=9, v=3),             # (S - 1) * Nc >= C
+        dict(i=15, v=16),           # workspace too small
+        dict(i=1, v=1022),          # compressed size not a multiple of 4
+    ]
+    for case in bad:
+        args = list(ok)
+        args[case["i"]] = case["v"]
+        assert lib.tans_fp8_gemm_fused(*args) == -1, case
+    assert lib.tans_fp8_gemm_raw(d, 128, 100, d, 1, f, d, None) == -1     # C % 16
+    assert lib.tans_fp8_gemm_raw(d, 128, 96, d, 9, f, d, None) == -1      # batch
+    ws = ctypes.c_int64()
+    assert lib.tans_gpu_encode_workspace(64, 15, 12, ctypes.byref(ws)) == -1
+    assert lib.tans_gpu_encode_workspace(64, 16, 10, ctypes.byref(ws)) == -1
+    assert lib.tans_gpu_encode_workspace(64, 16, 12, ctypes.byref(ws)) == 0 and ws.value > 0
+    assert lib.tans_gpu_encode_begin(d, 64, 16, d, d, 12, d, 16, d, d, d, d, None) == -1
+    assert b"workspace" in lib.tans_last_error()
+    assert lib.tans_gpu_encode_finish(64, 16, 12, d, d, d, 100, None) == -1
+
+
+def test_host_encode_table_matches_its_definition():
+    """enc_tab[s] = f_s | start_s << 16 and enc_next[start_s + rank] = L +
+    slot of the rank-th occurrence of s in slot order."""
+    import numpy as np
+    from rans_vectoradd import data as D, tans_codec as T
+    from rans_vectoradd._lib import lib
+    f = T.symbol_freqs(D.QWEN3_14B_FP8_EXP, "nibble")
+    sp = T.build_spread(f)
+    tab = np.empty(16, dtype=np.uint32)
+    nxt = np.empty(2048, dtype=np.uint16)
+    assert lib.tans_build_encode_table(sp.ctypes.data, f.ctypes.data, 16, 11, tab.ctypes.data,
+                                       nxt.ctypes.data) == 0
+    start = np.concatenate([[0], np.cumsum(f)[:-1]])
+    assert np.array_equal(tab & 0xFFFF, f) and np.array_equal(tab >> 16, start)
+    for s in range(16):
+        slots = np.nonzero(sp == s)[0]
+        assert np.array_equal(nxt[start[s]:start[s] + f[s]], 2048 + slots)
+    bad = sp.copy()
+    bad[0] = 99
+    assert lib.tans_build_encode_table(bad.ctypes.data, f.ctypes.data, 16, 11, tab.ctypes.data,
+                                       nxt.ctypes.data) != 0
