@@ -148,7 +148,7 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
  * the split of rans_vectoradd/tans_codec.py:109-124), from FP8 bytes already
  * on the device.  Three calls:
  *   workspace  bytes of device scratch begin and finish need for [K, N]
- *   begin      fp8 [K, N] (device, N even), enc_tab/enc_next from
+ *   begin      fp8 [K, N] (device, 16-byte aligned, N even), enc_tab/enc_next from
  *              tans_build_encode_table (device copies), log2L 12 (pair) or
  *              11 (nibble).  Writes offsets [ceil(K/64) + 1] (int64 words),
  *              states [K], sm tiles (layout above), and sets *status (device

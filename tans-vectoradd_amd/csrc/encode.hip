@@ -317,6 +317,8 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
     if (!fp8 || !enc_tab || !enc_next || !workspace || !offsets || !states || !sm || !status)
         return fail(TANS_EINVAL, "gpu_encode: null pointer");
     if (workspace_bytes < need) return fail(TANS_EINVAL, "gpu_encode: workspace too small");
+    if (reinterpret_cast<uintptr_t>(fp8) % 16)
+        return fail(TANS_EINVAL, "gpu_encode: fp8 must be 16-byte aligned");
     const int sps = log2L == TANS_PAIR_LOG2L ? 2 : 1;
     const int64_t S = N / sps;
     const int64_t G = (K + kLanes - 1) / kLanes;

@@ -301,6 +301,8 @@ def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: s
           "encode_gpu")
     dev = fp8_bytes.device
     x = fp8_bytes.contiguous()
+    if x.data_ptr() % 16:            # the kernels read 4- and 16-byte words
+        x = x.clone()
     G = -(-K // TANS_LANES)
     with torch.cuda.device(dev):
         ws_bytes = ctypes.c_int64()

@@ -72,6 +72,14 @@ def test_gpu_encode_edge_cases(R):
     fp8[5, 3] = 9 << 3
     with pytest.raises(RuntimeError, match="frequency is 0"):
         T.encode_gpu(fp8.cuda(), hist, alphabet="nibble")
+    # a misaligned view (row offset of 2 bytes) encodes like a fresh copy
+    torch.manual_seed(5)
+    big = R.random_fp8_bytes(65 * 34, device="cpu").reshape(65, 34)
+    view = big.cuda().reshape(-1)[2:2 + 64 * 34].reshape(64, 34)
+    assert view.data_ptr() % 16 != 0
+    a = T.encode_gpu(view, exp)
+    b = T.encode(view.cpu().contiguous(), exp)
+    assert torch.equal(a[0].cpu(), b[0]) and torch.equal(a[4].cpu(), b[4])
     with pytest.raises(ValueError):
         T.encode_gpu(torch.zeros((4, 16), dtype=torch.uint8), exp)       # CPU tensor
     with pytest.raises(ValueError):
