@@ -7,7 +7,10 @@
  * null stream).  Launches are asynchronous on `stream`; the return code
  * covers argument validation and the launch itself.  All functions return
  * TANS_OK (0) or a negative TANS_E* code; tans_last_error() gives a message
- * for the calling thread's last failure.
+ * for the calling thread's last failure.  Device buffers read or written
+ * with vector loads must be aligned: FP8 inputs/outputs of the raw kernels,
+ * compressed streams and the fused output 16 bytes, sign/mantissa tiles,
+ * offsets and tables 8 bytes (TANS_EINVAL otherwise).
  *
  * Data format ("wave64 lane layout"):
  *   - The input is K lanes (rows) of N FP8 E4M3FN bytes.  A lane is one tANS

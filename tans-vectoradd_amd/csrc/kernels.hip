@@ -1100,6 +1100,8 @@ int hip_check(hipError_t e, const char* what) {
     return fail(TANS_EHIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+bool aligned(const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
 int sps_for(int32_t log2L) {
     return log2L == TANS_PAIR_LOG2L ? 2 : (log2L == TANS_NIBBLE_LOG2L ? 1 : 0);
 }
@@ -1114,6 +1116,7 @@ extern "C" {
 int tans_fp8_memcpy(const void* a, void* c, int64_t n, void* stream) {
     if (n < 0 || n % 16 || ((!a || !c) && n)) return fail(TANS_EINVAL, "memcpy: n must be a multiple of 16");
     if (n == 0) return TANS_OK;
+    if (!aligned(a, 16) || !aligned(c, 16)) return fail(TANS_EINVAL, "memcpy: buffers must be 16-byte aligned");
     const int64_t n_vec = n / 16;
     const int64_t blocks = (n_vec + kBlock - 1) / kBlock;
     hipLaunchKernelGGL(fp8_copy_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream,
@@ -1124,6 +1127,8 @@ int tans_fp8_memcpy(const void* a, void* c, int64_t n, void* stream) {
 int tans_fp8_vecadd_raw(const void* a, const void* b, void* c, int64_t n, void* stream) {
     if (n < 0 || n % 16 || ((!a || !b || !c) && n)) return fail(TANS_EINVAL, "vecadd_raw: n must be a multiple of 16");
     if (n == 0) return TANS_OK;
+    if (!aligned(a, 16) || !aligned(b, 16) || !aligned(c, 16))
+        return fail(TANS_EINVAL, "vecadd_raw: buffers must be 16-byte aligned");
     const int64_t n_vec = n / 16;
     const int64_t blocks = (n_vec + kBlock - 1) / kBlock;
     hipLaunchKernelGGL(fp8_add_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream,
@@ -1155,6 +1160,10 @@ int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes, const int64_
         return fail(TANS_EINVAL, "vecadd_fused: null pointer");
     if (a_comp_bytes < 0 || b_comp_bytes < 0 || a_comp_bytes % 4 || b_comp_bytes % 4)
         return fail(TANS_EINVAL, "vecadd_fused: compressed sizes must be multiples of 4 bytes");
+    if (!aligned(a_comp, 16) || !aligned(b_comp, 16) || !aligned(a_sm, 8) || !aligned(b_sm, 8) ||
+        !aligned(a_offsets, 8) || !aligned(b_offsets, 8) || !aligned(a_states, 2) ||
+        !aligned(b_states, 2) || !aligned(table, 8) || !aligned(out, 16))
+        return fail(TANS_EINVAL, "vecadd_fused: misaligned buffer (comp and out 16, sm 8 bytes)");
     if (N / kTile > INT32_MAX) return fail(TANS_EINVAL, "vecadd_fused: N too large");
     const int64_t groups = (K + kLanes - 1) / kLanes;
     const int64_t per_block = (int64_t)kDecWaves * (sps == 2 ? kFusedGroups<2> : kFusedGroups<1>);
@@ -1184,6 +1193,9 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
         return fail(TANS_EINVAL, "decode: null pointer");
     if (comp_bytes < 0 || comp_bytes % 4)
         return fail(TANS_EINVAL, "decode: compressed size must be a multiple of 4 bytes");
+    if (!aligned(comp, 16) || !aligned(sm, 8) || !aligned(offsets, 8) || !aligned(states, 2) ||
+        !aligned(table, 8) || !aligned(out, 4))
+        return fail(TANS_EINVAL, "decode: misaligned buffer (comp 16, sm 8, out 4 bytes)");
     if ((N + kTile - 1) / kTile > INT32_MAX) return fail(TANS_EINVAL, "decode: N too large");
     // the stores address 4 rows of a tile with 32-bit offsets
     if (K > (int64_t(1) << 30)) return fail(TANS_EINVAL, "decode: more than 2^30 lanes");
@@ -1219,6 +1231,9 @@ int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* off
         return fail(TANS_EINVAL, "gemm_fused: null pointer");
     if (comp_bytes < 0 || comp_bytes % 4)
         return fail(TANS_EINVAL, "gemm_fused: compressed size must be a multiple of 4 bytes");
+    if (!aligned(comp, 16) || !aligned(sm, 8) || !aligned(offsets, 8) || !aligned(states, 2) ||
+        !aligned(table, 8) || !aligned(x, 2) || !aligned(workspace, 4) || !aligned(y, 2))
+        return fail(TANS_EINVAL, "gemm_fused: misaligned buffer (comp 16, sm 8 bytes)");
     const int64_t Rp = (R + kLanes - 1) / kLanes * kLanes;
     if (workspace_bytes < S * B * Rp * 4)
         return fail(TANS_EINVAL, "gemm_fused: workspace smaller than S * B * Rp * 4 bytes");
@@ -1255,6 +1270,8 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
     if (R <= 0 || C <= 0 || C % 16) return fail(TANS_EINVAL, "gemm_raw: need R > 0 and C a positive multiple of 16");
     if (B < 1 || B > kGemmMaxBatch) return fail(TANS_EINVAL, "gemm_raw: batch must be 1..8");
     if (!w || !x || !y) return fail(TANS_EINVAL, "gemm_raw: null pointer");
+    if (!aligned(w, 16) || !aligned(x, 16) || !aligned(y, 2))
+        return fail(TANS_EINVAL, "gemm_raw: W and x must be 16-byte aligned");
     const int64_t rows_per_block = (256 / kLanes) * kRawRows;
     const int64_t blocks = (R + rows_per_block - 1) / rows_per_block;
     if (blocks > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: matrix too large");

@@ -136,3 +136,16 @@ def test_host_encode_table_matches_its_definition():
     bad[0] = 99
     assert lib.tans_build_encode_table(bad.ctypes.data, f.ctypes.data, 16, 11, tab.ctypes.data,
                                        nxt.ctypes.data) != 0
+
+
+def test_misaligned_buffers_are_rejected_before_launch():
+    from rans_vectoradd._lib import lib
+    P = ctypes.c_void_p
+    d, m = P(4096), P(4097 + 1)          # 16-byte aligned, 2 mod 16
+    assert lib.tans_fp8_vecadd_raw(m, d, d, 16, None) == -1
+    assert b"aligned" in lib.tans_last_error()
+    assert lib.tans_fp8_memcpy(d, m, 16, None) == -1
+    assert lib.tans_fp8_vecadd_fused(m, 1024, d, d, d, d, 1024, d, d, d, d, 12, 64, 16, d, None) == -1
+    assert lib.tans_decode(m, 1024, d, d, d, d, 12, 64, 16, d, None) == -1
+    f = ctypes.c_float(1.0)
+    assert lib.tans_fp8_gemm_raw(d, 128, 96, m, 1, f, d, None) == -1
