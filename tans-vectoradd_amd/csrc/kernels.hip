@@ -306,11 +306,13 @@ __device__ __forceinline__ void feed_advance(Feed& f) {
     f.next_slot = f.next_slot == (uint32_t)(kSlots - 1) ? 0u : f.next_slot + 1;
 }
 
-// Clamp group g's stream to the buffer, fetch and write its first kSlots
-// segments.
-__device__ __forceinline__ void feed_init(Feed& f, const uint32_t* comp, int64_t words,
-                                          const int64_t* off, int64_t g, uint32_t* ring, int lane,
-                                          Seg (&pend)[kDelay]) {
+// Clamp group g's stream to the buffer and fetch its first kSlots segments
+// into `first`; feed_commit writes them to the ring.  The two halves let a
+// kernel issue these loads together with the decode table's, so the stream
+// and the table cost one memory round trip before decoding starts.
+__device__ __forceinline__ void feed_fetch(Feed& f, const uint32_t* comp, int64_t words,
+                                           const int64_t* off, int64_t g, uint32_t* ring, int lane,
+                                           Seg (&first)[kSlots]) {
     int64_t s = off[g], e = off[g + 1];
     s = s < 0 ? 0 : (s > words ? words : s);
     e = e < s ? s : (e > words ? words : e);
@@ -323,14 +325,17 @@ __device__ __forceinline__ void feed_init(Feed& f, const uint32_t* comp, int64_t
     f.handed = 0;
     f.ring_b = 0;
     f.ring = ring;
-    Seg first[kSlots];
     #pragma unroll
     for (int i = 0; i < kSlots; i++) {
         first[i] = fetch_seg(f, f.next_word < f.len, lane);
         feed_advance(f);
     }
+}
+
+__device__ __forceinline__ void feed_commit(Feed& f, int lane, const Seg (&first)[kSlots],
+                                            Seg (&pend)[kDelay]) {
     #pragma unroll
-    for (int i = 0; i < kSlots; i++) write_seg(ring, i, first[i], lane);
+    for (int i = 0; i < kSlots; i++) write_seg(f.ring, i, first[i], lane);
     #pragma unroll
     for (int i = 0; i < kDelay; i++) {
         f.dest[i] = -1;
@@ -415,18 +420,34 @@ __device__ __forceinline__ void compose8(uint32_t ex_lo, uint32_t ex_hi, uint32_
     out_hi = bfi(kExpMask, ex_hi, __builtin_amdgcn_alignbit(smw, smw, 4u));
 }
 
-// Copy the decode table into LDS.  Entries that would step outside the
-// table (nb > log2L or base + 2^nb > 2L) are replaced by a harmless one, so
-// a malformed table gives wrong bytes, never an out-of-range LDS access.
+// The decode table is copied into LDS by the kDecBlock threads of a
+// decoder workgroup in two halves: table_fetch issues every load of the
+// thread, table_store writes them once they arrive.  Entries that would
+// step outside the table (nb > log2L or base + 2^nb > 2L) are replaced by a
+// harmless one, so a malformed table gives wrong bytes, never an
+// out-of-range LDS access.
 template <uint32_t L>
-__device__ __forceinline__ void load_table(v2u* lds, const v2u* __restrict__ table) {
+struct TableRegs {
+    static_assert(L % kDecBlock == 0, "the table is split evenly over the workgroup");
+    v2u e[L / kDecBlock];
+};
+
+template <uint32_t L>
+__device__ __forceinline__ void table_fetch(TableRegs<L>& r, const v2u* __restrict__ table) {
+    #pragma unroll
+    for (uint32_t k = 0; k < L / kDecBlock; k++) r.e[k] = table[threadIdx.x + k * kDecBlock];
+}
+
+template <uint32_t L>
+__device__ __forceinline__ void table_store(v2u* lds, const TableRegs<L>& r) {
     constexpr uint32_t log2L = 31 - __builtin_clz(L);
-    for (uint32_t i = threadIdx.x; i < L; i += blockDim.x) {
-        v2u e = table[i];
+    #pragma unroll
+    for (uint32_t k = 0; k < L / kDecBlock; k++) {
+        v2u e = r.e[k];
         const uint32_t nb = e.x & 0xFFu;
         const uint32_t base = e.y >> 3;
         if (nb > log2L || (e.y & 7u) || base + (1u << nb) > L) e = v2u{e.x & ~0xFFu, 0u};
-        lds[i] = e;
+        lds[threadIdx.x + k * kDecBlock] = e;
     }
 }
 
@@ -572,13 +593,15 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     constexpr int C = 2 * G;
     __shared__ DecSmem<SPS, C> smem;
     v2u* tbl = smem.tbl;
-    load_table<L>(tbl, table);
-    if (threadIdx.x == 0) smem.progress = 0;
-    __syncthreads();
+    // issue the table, stream, state and sign/mantissa loads together; a
+    // wave past the last group loads the last one and leaves after the
+    // barrier
+    TableRegs<L> tr;
+    table_fetch<L>(tr, table);
     const int lane = threadIdx.x & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     const int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
-    if (g0 * kLanes >= K) return;   // wave-uniform
+    const bool live = g0 * kLanes < K;   // wave-uniform
     const int64_t n_groups = (K + kLanes - 1) / kLanes;
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * G;
     FusedWave<SPS, G> w;
@@ -589,6 +612,9 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     w.tbl = tbl;
     w.sm_stride = K * 8;
     w.out_stride = K * 16;
+    Seg first[C][kSlots];
+    uint16_t st0[C];
+    bool act[C];
     #pragma unroll
     for (int j = 0; j < G; j++) {
         // a wave past the last group repeats it with no lanes in range
@@ -599,12 +625,13 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
         const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
         w.sm_bytes[j] = (uint32_t)lanes * 8u;
         w.out_cur[j] = reinterpret_cast<char*>(out + k0);
-        feed_init(w.ch.f[2 * j], a_comp, a_words, a_off, g, smem.rings[wave][2 * j], lane,
-                  w.ch.p[2 * j]);
-        feed_init(w.ch.f[2 * j + 1], b_comp, b_words, b_off, g, smem.rings[wave][2 * j + 1], lane,
-                  w.ch.p[2 * j + 1]);
-        lane_init(w.ch.l[2 * j], active, a_st[k0 + lane_ld], L);
-        lane_init(w.ch.l[2 * j + 1], active, b_st[k0 + lane_ld], L);
+        feed_fetch(w.ch.f[2 * j], a_comp, a_words, a_off, g, smem.rings[wave][2 * j], lane,
+                   first[2 * j]);
+        feed_fetch(w.ch.f[2 * j + 1], b_comp, b_words, b_off, g, smem.rings[wave][2 * j + 1],
+                   lane, first[2 * j + 1]);
+        st0[2 * j] = a_st[k0 + lane_ld];
+        st0[2 * j + 1] = b_st[k0 + lane_ld];
+        act[2 * j] = act[2 * j + 1] = active;
         const char* rows[2] = {reinterpret_cast<const char*>(a_sm + k0),
                                reinterpret_cast<const char*>(b_sm + k0)};
         #pragma unroll
@@ -619,6 +646,15 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             const int64_t tn = kSmAhead < n_tiles ? kSmAhead : n_tiles - 1;
             w.pf[c] = rows[s] + tn * w.sm_stride;
         }
+    }
+    table_store<L>(tbl, tr);
+    if (threadIdx.x == 0) smem.progress = 0;
+    __syncthreads();
+    if (!live) return;
+    #pragma unroll
+    for (int c = 0; c < C; c++) {
+        feed_commit(w.ch.f[c], lane, first[c], w.ch.p[c]);
+        lane_init(w.ch.l[c], act[c], st0[c], L);
     }
     int t = 0;
     for (; t + kSmAhead <= n_tiles; t += kSmAhead) {
@@ -766,13 +802,13 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     constexpr int C = kDecodeGroups;
     __shared__ DecSmem<SPS, C> smem;
     v2u* tbl = smem.tbl;
-    load_table<L>(tbl, table);
-    if (threadIdx.x == 0) smem.progress = 0;
-    __syncthreads();
+    // loads issued together, as in fused_add_kernel
+    TableRegs<L> tr;
+    table_fetch<L>(tr, table);
     const int lane = threadIdx.x & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     const int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * C;
-    if (g0 * kLanes >= K) return;   // wave-uniform
+    const bool live = g0 * kLanes < K;   // wave-uniform
     const int64_t n_groups = (K + kLanes - 1) / kLanes;
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * C;
     DecodeWave<SPS> w;
@@ -788,6 +824,9 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     w.qoff = (uint32_t)(lane & 3) * (uint32_t)K + (uint32_t)(lane >> 2) * 4u;
     quad_selectors(lane, w.sel1, w.sel2);
     bool full = true;
+    Seg first[C][kSlots];
+    uint16_t st0[C];
+    bool act[C];
     #pragma unroll
     for (int j = 0; j < C; j++) {
         // a wave past the last group repeats it with no lanes in range
@@ -799,8 +838,9 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
         const bool active = lane < lanes;
         const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
         w.sm_bytes[j] = (uint32_t)lanes * 8u;
-        feed_init(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], lane, w.ch.p[j]);
-        lane_init(w.ch.l[j], active, st[k0 + lane_ld], L);
+        feed_fetch(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], lane, first[j]);
+        st0[j] = st[k0 + lane_ld];
+        act[j] = active;
         const char* row = reinterpret_cast<const char*>(sm + k0);
         #pragma unroll
         for (int i = 0; i < kSmAhead; i++) {
@@ -812,6 +852,15 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
         w.pf[j] = row + tn * w.sm_stride;
     }
     w.full = full;
+    table_store<L>(tbl, tr);
+    if (threadIdx.x == 0) smem.progress = 0;
+    __syncthreads();
+    if (!live) return;
+    #pragma unroll
+    for (int j = 0; j < C; j++) {
+        feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
+        lane_init(w.ch.l[j], act[j], st0[j], L);
+    }
     w.run(rag ? rag : kTile);
 }
 
@@ -940,32 +989,38 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     // stage x[b][s * Nc + c] for c < Nc16 (zero past the segment or the matrix)
     const int nc16 = (Nc + kTile - 1) / kTile * kTile;
     const uint32_t x_row = (uint32_t)nc16 / 2;
-    uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem.xs);
-    for (int i = threadIdx.x; i < NB * nc16; i += blockDim.x) {
+    // issue the x, table, stream, state and sign/mantissa loads together
+    // (as in fused_add_kernel); a wave past the last row group loads the
+    // last one and leaves after the barrier
+    constexpr int kXPer = kGemmMaxBatch * kGemmMaxSegCols / kDecBlock;
+    uint16_t xv[kXPer];
+    #pragma unroll
+    for (int k = 0; k < kXPer; k++) {
+        const int i = (int)threadIdx.x + k * kDecBlock;
         const int b = i / nc16, c = i % nc16;
         const int64_t col = (int64_t)s * Nc + c;
-        xs16[i] = (c < Nc && col < C) ? x[(int64_t)b * C + col] : (uint16_t)0;
+        xv[k] = (i < NB * nc16 && c < Nc && col < C) ? x[(int64_t)b * C + col] : (uint16_t)0;
     }
-    v2u* tbl = smem.dec.tbl;
-    load_table<L>(tbl, table);
-    if (threadIdx.x == 0) smem.dec.progress = 0;
-    __syncthreads();
+    TableRegs<L> tr;
+    table_fetch<L>(tr, table);
     const int lane = threadIdx.x & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     const int64_t rg0 = (int64_t)rb * kGemmGroupsPerBlock + (int64_t)wave * CH;
-    if (rg0 >= n_rg) return;   // wave-uniform
+    const bool live = rg0 < n_rg;   // wave-uniform
     const int64_t rg_left = n_rg - (int64_t)rb * kGemmGroupsPerBlock;
     GemmWave<SPS, NB> w;
     w.progress = &smem.dec.progress;
     w.live = (uint32_t)(rg_left >= kGemmGroupsPerBlock ? kDecWaves : (rg_left + CH - 1) / CH);
     w.lane = lane;
-    w.tbl = tbl;
+    w.tbl = smem.dec.tbl;
     w.xs = smem.xs;
     w.x_row = x_row;
     w.sm_stride = (int64_t)S * Rp * 8;                      // lanes: S * Rp
     const int rag = Nc % kTile;
     w.n_tiles = Nc / kTile + (rag ? 1 : 0);
     w.sm_bytes = kLanes * 8u;
+    Seg first[CH][kSlots];
+    uint16_t st0[CH];
     #pragma unroll
     for (int j = 0; j < CH; j++) {
         // a wave with one row group left repeats it as its second chain and
@@ -973,8 +1028,8 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
         const int64_t rg = rg0 + j < n_rg ? rg0 + j : n_rg - 1;
         const int64_t g = (int64_t)s * n_rg + rg;
         const int64_t k0 = g * kLanes;
-        feed_init(w.ch.f[j], comp, words, off, g, smem.dec.rings[wave][j], lane, w.ch.p[j]);
-        lane_init(w.ch.l[j], true, st[k0 + lane], L);
+        feed_fetch(w.ch.f[j], comp, words, off, g, smem.dec.rings[wave][j], lane, first[j]);
+        st0[j] = st[k0 + lane];
         const char* row = reinterpret_cast<const char*>(sm + k0);
         #pragma unroll
         for (int i = 0; i < kSmAhead; i++) {
@@ -986,6 +1041,21 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
         w.pf[j] = row + tn * w.sm_stride;
         #pragma unroll
         for (int b = 0; b < NB; b++) w.acc[j][b] = 0.0f;
+    }
+    uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem.xs);
+    #pragma unroll
+    for (int k = 0; k < kXPer; k++) {
+        const int i = (int)threadIdx.x + k * kDecBlock;
+        if (i < NB * nc16) xs16[i] = xv[k];
+    }
+    table_store<L>(smem.dec.tbl, tr);
+    if (threadIdx.x == 0) smem.dec.progress = 0;
+    __syncthreads();
+    if (!live) return;
+    #pragma unroll
+    for (int j = 0; j < CH; j++) {
+        feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
+        lane_init(w.ch.l[j], true, st0[j], L);
     }
     w.run(rag ? rag : kTile);
     #pragma unroll
