@@ -891,7 +891,7 @@ constexpr int kGemmMaxSegCols = 512;                  // Nc limit: the x stage i
 template <int SPS>
 struct GemmSmem {
     DecSmem<SPS, kGemmChains> dec;
-    uint32_t xs[kGemmMaxBatch * kGemmMaxSegCols / 2];  // bf16 pairs [B][Nc16 / 2]
+    uint32_t xs[kGemmMaxBatch * kGemmMaxSegCols / 2];  // bf16 pairs [B][kGemmMaxSegCols / 2]
 };
 
 template <int SPS, int NB>
@@ -903,7 +903,6 @@ struct GemmWave {
     uint32_t sm_bytes;
     const v2u* tbl;
     const uint32_t* xs;     // LDS x stage of the segment
-    uint32_t x_row;         // dwords per batch row in the stage
     uint32_t* progress;
     uint32_t live;
     int64_t sm_stride;
@@ -936,7 +935,7 @@ struct GemmWave {
         }
         #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const v4u* xp = reinterpret_cast<const v4u*>(xs + b * x_row + t * 8);
+            const v4u* xp = reinterpret_cast<const v4u*>(xs + b * (kGemmMaxSegCols / 2) + t * 8);
             const v4u x0 = xp[0];
             const v4u x1 = xp[1];
             const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -986,20 +985,25 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     const int s = (int)(blockIdx.x / (unsigned)row_blocks);
     const int rb = (int)(blockIdx.x % (unsigned)row_blocks);
     const int64_t n_rg = Rp / kLanes;                       // row groups per segment
-    // stage x[b][s * Nc + c] for c < Nc16 (zero past the segment or the matrix)
-    const int nc16 = (Nc + kTile - 1) / kTile * kTile;
-    const uint32_t x_row = (uint32_t)nc16 / 2;
     // issue the x, table, stream, state and sign/mantissa loads together
     // (as in fused_add_kernel); a wave past the last row group loads the
-    // last one and leaves after the barrier
-    constexpr int kXPer = kGemmMaxBatch * kGemmMaxSegCols / kDecBlock;
+    // last one and leaves after the barrier.  x[b][s * Nc + c] is staged at
+    // xs[b][c] (rows of kGemmMaxSegCols), zero past the segment or the
+    // matrix: thread i takes column i % kGemmMaxSegCols of batch rows
+    // i / kGemmMaxSegCols + kXRows * k.
+    constexpr int kXRows = kDecBlock / kGemmMaxSegCols;
+    constexpr int kXPer = kGemmMaxBatch / kXRows;
+    static_assert(kXRows * kGemmMaxSegCols == kDecBlock && kXPer * kXRows == kGemmMaxBatch,
+                  "the x stage is split evenly over the workgroup");
+    const int xc = (int)threadIdx.x % kGemmMaxSegCols;
+    const int xb = (int)threadIdx.x / kGemmMaxSegCols;
+    const int64_t xcol = (int64_t)s * Nc + xc;
+    const bool x_in = xc < Nc && xcol < C;
     uint16_t xv[kXPer];
     #pragma unroll
     for (int k = 0; k < kXPer; k++) {
-        const int i = (int)threadIdx.x + k * kDecBlock;
-        const int b = i / nc16, c = i % nc16;
-        const int64_t col = (int64_t)s * Nc + c;
-        xv[k] = (i < NB * nc16 && c < Nc && col < C) ? x[(int64_t)b * C + col] : (uint16_t)0;
+        const int b = xb + kXRows * k;
+        xv[k] = (b < NB && x_in) ? x[(int64_t)b * C + xcol] : (uint16_t)0;
     }
     TableRegs<L> tr;
     table_fetch<L>(tr, table);
@@ -1014,7 +1018,6 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     w.lane = lane;
     w.tbl = smem.dec.tbl;
     w.xs = smem.xs;
-    w.x_row = x_row;
     w.sm_stride = (int64_t)S * Rp * 8;                      // lanes: S * Rp
     const int rag = Nc % kTile;
     w.n_tiles = Nc / kTile + (rag ? 1 : 0);
@@ -1045,8 +1048,8 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem.xs);
     #pragma unroll
     for (int k = 0; k < kXPer; k++) {
-        const int i = (int)threadIdx.x + k * kDecBlock;
-        if (i < NB * nc16) xs16[i] = xv[k];
+        const int b = xb + kXRows * k;
+        if (b < NB) xs16[b * kGemmMaxSegCols + xc] = xv[k];
     }
     table_store<L>(smem.dec.tbl, tr);
     if (threadIdx.x == 0) smem.dec.progress = 0;
