@@ -701,6 +701,21 @@ __device__ __forceinline__ void quad_selectors(int lane, uint32_t& sel1, uint32_
     sel2 = (lane & 1) ? 0x03070105u : 0x06020400u;
 }
 
+// Row-major staging of 8 output rows x 128 columns per wave (the wave's two
+// groups) for whole-line stores.  Rows are kXposeStride dwords apart: 48 is
+// 16 mod 32, so the four rows a quad writes fall in alternating halves of
+// the banks.  The last row needs no padding.
+constexpr int kXposeStride = 48;
+constexpr int kXposeWords = 7 * kXposeStride + kDecodeGroups * kLanes / 4;
+
+template <int SPS>
+struct DecodeSmem {
+    DecSmem<SPS, kDecodeGroups> dec;
+    alignas(16) uint32_t xpose[kDecWaves][kXposeWords];
+};
+static_assert(sizeof(DecodeSmem<2>) <= 160 * 1024 && sizeof(DecodeSmem<1>) <= 160 * 1024,
+              "decoder LDS exceeds the 160 KiB of a gfx950 CU");
+
 template <int SPS>
 struct DecodeWave {
     static constexpr int C = kDecodeGroups;
@@ -717,9 +732,11 @@ struct DecodeWave {
     int64_t sm_stride;      // K * 8
     uint32_t qoff;          // (lane & 3) * K + (lane >> 2) * 4: the lane's word after the transpose
     uint32_t sel1, sel2;
+    uint32_t* xp;           // this wave's staging rows (LDS)
     int n_tiles;
     int lane;
     bool full;              // both groups have 64 lanes in range (wave-uniform)
+    bool lines;             // K % 16 == 0: rows start 16-byte aligned
 
     // Tile t (P = t mod kSmAhead) holding n elements per lane (n < 16 only
     // for a ragged last tile).
@@ -738,7 +755,28 @@ struct DecodeWave {
             compose8(ex[g][0], ex[g][1], sm[g][P].x, w[g][0], w[g][1]);
             compose8(ex[g][2], ex[g][3], sm[g][P].y, w[g][2], w[g][3]);
         }
-        if (full && n == kTile) {   // wave-uniform
+        if (full && n == kTile && lines) {   // wave-uniform
+            // rows 8h .. 8h + 7 of both groups go through the staging rows;
+            // lane l then stores columns 16 (l & 7) .. + 15 of row 8h + l / 8,
+            // so each 8 lanes write one whole 128-byte line (non-temporal).
+            // The wave's LDS accesses execute in order, so the writes of
+            // half h = 1 come after the reads of half 0.
+            #pragma unroll
+            for (int h = 0; h < 2; h++) {
+                #pragma unroll
+                for (int g = 0; g < C; g++) {
+                    #pragma unroll
+                    for (int jj = 0; jj < 2; jj++)
+                        xp[(4 * jj + (lane & 3)) * kXposeStride + 16 * g + (lane >> 2)] =
+                            quad_transpose(w[g][2 * h + jj], sel1, sel2);
+                }
+                const v4u v = *reinterpret_cast<const v4u*>(xp + (lane >> 3) * kXposeStride +
+                                                            (lane & 7) * 4);
+                __builtin_nontemporal_store(
+                    v, reinterpret_cast<v4u*>(out_tile + (int64_t)(8 * h + (lane >> 3)) * K +
+                                              (lane & 7) * 16));
+            }
+        } else if (full && n == kTile) {
             #pragma unroll
             for (int g = 0; g < C; g++) {
                 #pragma unroll
@@ -800,7 +838,8 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     const v2u* __restrict__ table, int64_t K, int64_t N, uint8_t* __restrict__ out) {
     constexpr uint32_t L = Alpha<SPS>::L;
     constexpr int C = kDecodeGroups;
-    __shared__ DecSmem<SPS, C> smem;
+    __shared__ DecodeSmem<SPS> dsmem;
+    DecSmem<SPS, C>& smem = dsmem.dec;
     v2u* tbl = smem.tbl;
     // loads issued together, as in fused_add_kernel
     TableRegs<L> tr;
@@ -823,6 +862,8 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     w.out_tile = out + g0 * kLanes;
     w.qoff = (uint32_t)(lane & 3) * (uint32_t)K + (uint32_t)(lane >> 2) * 4u;
     quad_selectors(lane, w.sel1, w.sel2);
+    w.xp = dsmem.xpose[wave];
+    w.lines = K % 16 == 0;
     bool full = true;
     Seg first[C][kSlots];
     uint16_t st0[C];

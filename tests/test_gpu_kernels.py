@@ -102,12 +102,15 @@ def test_table_device_any_spread(R, alphabet):
 @pytest.mark.parametrize("alphabet", ALPHABETS)
 @pytest.mark.parametrize("K,N", [(128, 128), (1024, 128), (10000, 128), (100000, 128),
                                  (64, 2), (65, 18), (200, 130), (3, 1000),
-                                 (130, 30), (192, 64), (66, 80), (1, 16), (4096, 14)])
+                                 (130, 30), (192, 64), (66, 80), (1, 16), (4096, 14),
+                                 (2064, 48)])
 def test_decode_roundtrip(R, alphabet, K, N):
     """The reference's cases (test_gpu_decode_tans.py:69-74) plus ragged
     ones: partial last groups of 1, 2, 3, 8, 16, 32 lanes, a wave holding one
     complete group and no second one (K = 192), and last tiles of 2, 8, 14
-    elements."""
+    elements.  Complete waves store whole lines when K % 16 == 0 (rows 16-byte
+    aligned but not line-aligned at K = 10000 and 2064) and single words
+    otherwise (K = 200, 130)."""
     from rans_vectoradd import tans_codec as T
     _say(f"case: gpu_tans_decode K={K} N={N} {alphabet}")
     exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
