@@ -675,11 +675,14 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
 //
 // A tile leaves each lane with 16 bytes of its own column (rows 16t ..
 // 16t + 15).  A 4x4 byte transpose inside each quad of lanes (two DPP swaps
-// and two v_perm per word) turns every word into 4 columns of one row, so a
-// dword store per word writes 4 rows x 64 bytes and the wave's two groups
-// fill each 128-byte line of a row between them.  In a wave whose groups
-// are not both complete (the tensor's last lanes) each store is checked
-// against the lanes in range, down to single bytes.
+// and two v_perm per word) turns every word into 4 columns of one row.  When
+// rows start 16-byte aligned (K % 16 == 0) and both groups are complete,
+// the words of 8 rows go through LDS staging rows, and each lane stores 16
+// consecutive columns of one row: every 8 lanes write a whole 128-byte line,
+// non-temporally.  Otherwise each word is stored where it lands (4 rows x 64
+// bytes per store instruction), and in a wave whose groups are not both
+// complete (the tensor's last lanes) each store is checked against the
+// lanes in range, down to single bytes.
 // ---------------------------------------------------------------------
 constexpr int kDecodeGroups = 2;
 
