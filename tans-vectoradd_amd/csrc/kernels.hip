@@ -43,6 +43,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <atomic>
 #include <climits>
 #include <string>
 #include <type_traits>
@@ -532,7 +534,11 @@ __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ 
 
 // ---------------------------------------------------------------------
 // Fused decode + add.  A wave decodes G groups of A and the same G groups
-// of B (C = 2G chains) and writes their sums, tiled [N/16, K, 16].
+// of B (C = 2G chains) and writes their sums, tiled [N/16, K, 16].  The
+// grid holds at most one workgroup per CU (the LDS allows no more), and a
+// wave takes groups g, g + grid groups, ... in turn: the decode table is
+// loaded once per CU, and short streams (down to one tile per lane) do not
+// pay a workgroup launch and a table load per group.
 // ---------------------------------------------------------------------
 template <int SPS, int G>
 struct FusedWave {
@@ -549,13 +555,14 @@ struct FusedWave {
     int64_t out_stride;     // K * 16
     int n_tiles;
     int lane;
+    int base;               // tiles this wave finished in earlier groups (pacing)
 
     // Tile t, with P = t mod kSmAhead.
     template <int P>
     __device__ __forceinline__ void tile(int t) {
         uint32_t ex[C][4];
         dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, C>(ch, tbl, lane, ex);
-        pace(progress, lane, (uint32_t)t, live);
+        pace(progress, lane, (uint32_t)(base + t), live);
         #pragma unroll
         for (int g = 0; g < G; g++) {
             uint32_t wa[4], wb[4];
@@ -600,9 +607,10 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     table_fetch<L>(tr, table);
     const int lane = threadIdx.x & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
-    const int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
-    const bool live = g0 * kLanes < K;   // wave-uniform
     const int64_t n_groups = (K + kLanes - 1) / kLanes;
+    const int64_t grid_groups = (int64_t)gridDim.x * kDecWaves * G;   // groups per round
+    int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
+    const bool live = g0 < n_groups;   // wave-uniform
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * G;
     FusedWave<SPS, G> w;
     w.progress = &smem.progress;
@@ -615,58 +623,70 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     Seg first[C][kSlots];
     uint16_t st0[C];
     bool act[C];
-    #pragma unroll
-    for (int j = 0; j < G; j++) {
-        // a wave past the last group repeats it with no lanes in range
-        const int64_t g = g0 + j < n_groups ? g0 + j : n_groups - 1;
-        const int64_t k0 = g * kLanes;
-        const int lanes = g0 + j < n_groups ? (K - k0 < kLanes ? (int)(K - k0) : kLanes) : 0;
-        const bool active = lane < lanes;
-        const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
-        w.sm_bytes[j] = (uint32_t)lanes * 8u;
-        w.out_cur[j] = reinterpret_cast<char*>(out + k0);
-        feed_fetch(w.ch.f[2 * j], a_comp, a_words, a_off, g, smem.rings[wave][2 * j], lane,
-                   first[2 * j]);
-        feed_fetch(w.ch.f[2 * j + 1], b_comp, b_words, b_off, g, smem.rings[wave][2 * j + 1],
-                   lane, first[2 * j + 1]);
-        st0[2 * j] = a_st[k0 + lane_ld];
-        st0[2 * j + 1] = b_st[k0 + lane_ld];
-        act[2 * j] = act[2 * j + 1] = active;
-        const char* rows[2] = {reinterpret_cast<const char*>(a_sm + k0),
-                               reinterpret_cast<const char*>(b_sm + k0)};
+    // the loads of the groups gbase .. gbase + G - 1
+    auto setup = [&](int64_t gbase) {
         #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            const int c = 2 * j + s;
+        for (int j = 0; j < G; j++) {
+            // a wave past the last group repeats it with no lanes in range
+            const int64_t g = gbase + j < n_groups ? gbase + j : n_groups - 1;
+            const int64_t k0 = g * kLanes;
+            const int lanes = gbase + j < n_groups ? (K - k0 < kLanes ? (int)(K - k0) : kLanes) : 0;
+            const bool active = lane < lanes;
+            const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
+            w.sm_bytes[j] = (uint32_t)lanes * 8u;
+            w.out_cur[j] = reinterpret_cast<char*>(out + k0);
+            feed_fetch(w.ch.f[2 * j], a_comp, a_words, a_off, g, smem.rings[wave][2 * j], lane,
+                       first[2 * j]);
+            feed_fetch(w.ch.f[2 * j + 1], b_comp, b_words, b_off, g, smem.rings[wave][2 * j + 1],
+                       lane, first[2 * j + 1]);
+            st0[2 * j] = a_st[k0 + lane_ld];
+            st0[2 * j + 1] = b_st[k0 + lane_ld];
+            act[2 * j] = act[2 * j + 1] = active;
+            const char* rows[2] = {reinterpret_cast<const char*>(a_sm + k0),
+                                   reinterpret_cast<const char*>(b_sm + k0)};
             #pragma unroll
-            for (int i = 0; i < kSmAhead; i++) {
-                const int64_t ti = i < n_tiles ? i : n_tiles - 1;
-                w.sm[c][i] = __builtin_amdgcn_raw_buffer_load_b64(
-                    rsrc(rows[s] + ti * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+            for (int s = 0; s < 2; s++) {
+                const int c = 2 * j + s;
+                #pragma unroll
+                for (int i = 0; i < kSmAhead; i++) {
+                    const int64_t ti = i < n_tiles ? i : n_tiles - 1;
+                    w.sm[c][i] = __builtin_amdgcn_raw_buffer_load_b64(
+                        rsrc(rows[s] + ti * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+                }
+                const int64_t tn = kSmAhead < n_tiles ? kSmAhead : n_tiles - 1;
+                w.pf[c] = rows[s] + tn * w.sm_stride;
             }
-            const int64_t tn = kSmAhead < n_tiles ? kSmAhead : n_tiles - 1;
-            w.pf[c] = rows[s] + tn * w.sm_stride;
         }
-    }
+    };
+    setup(g0);
     table_store<L>(tbl, tr);
     if (threadIdx.x == 0) smem.progress = 0;
     __syncthreads();
     if (!live) return;
-    #pragma unroll
-    for (int c = 0; c < C; c++) {
-        feed_commit(w.ch.f[c], lane, first[c], w.ch.p[c]);
-        lane_init(w.ch.l[c], act[c], st0[c], L);
+    int done = 0;   // tiles of earlier groups (the pacing count runs on)
+    for (;;) {
+        #pragma unroll
+        for (int c = 0; c < C; c++) {
+            feed_commit(w.ch.f[c], lane, first[c], w.ch.p[c]);
+            lane_init(w.ch.l[c], act[c], st0[c], L);
+        }
+        w.base = done;
+        int t = 0;
+        for (; t + kSmAhead <= n_tiles; t += kSmAhead) {
+            w.template tile<0>(t);
+            w.template tile<1>(t + 1);
+            w.template tile<2>(t + 2);
+            w.template tile<3>(t + 3);
+        }
+        static_assert(kSmAhead == 4, "the loop above is unrolled for kSmAhead == 4");
+        if (t < n_tiles) w.template tile<0>(t);
+        if (t + 1 < n_tiles) w.template tile<1>(t + 1);
+        if (t + 2 < n_tiles) w.template tile<2>(t + 2);
+        done += n_tiles;
+        g0 += grid_groups;
+        if (g0 >= n_groups) break;
+        setup(g0);
     }
-    int t = 0;
-    for (; t + kSmAhead <= n_tiles; t += kSmAhead) {
-        w.template tile<0>(t);
-        w.template tile<1>(t + 1);
-        w.template tile<2>(t + 2);
-        w.template tile<3>(t + 3);
-    }
-    static_assert(kSmAhead == 4, "the loop above is unrolled for kSmAhead == 4");
-    if (t < n_tiles) w.template tile<0>(t);
-    if (t + 1 < n_tiles) w.template tile<1>(t + 1);
-    if (t + 2 < n_tiles) w.template tile<2>(t + 2);
 }
 
 // ---------------------------------------------------------------------
@@ -1219,6 +1239,24 @@ int hip_check(hipError_t e, const char* what) {
 
 bool aligned(const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
+// Compute units of the current device, queried once per device.
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < kMaxDevices) {
+        const int known = g_cu_count[dev].load(std::memory_order_relaxed);
+        if (known > 0) return known;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    if (dev < kMaxDevices && cus > 0) g_cu_count[dev].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
 int sps_for(int32_t log2L) {
     return log2L == TANS_PAIR_LOG2L ? 2 : (log2L == TANS_NIBBLE_LOG2L ? 1 : 0);
 }
@@ -1284,8 +1322,10 @@ int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes, const int64_
     if (N / kTile > INT32_MAX) return fail(TANS_EINVAL, "vecadd_fused: N too large");
     const int64_t groups = (K + kLanes - 1) / kLanes;
     const int64_t per_block = (int64_t)kDecWaves * (sps == 2 ? kFusedGroups<2> : kFusedGroups<1>);
-    const int64_t blocks = (groups + per_block - 1) / per_block;
-    if (blocks > INT32_MAX) return fail(TANS_EINVAL, "vecadd_fused: K too large");
+    // one workgroup per CU at most; the waves loop over the groups
+    const int cus = cu_count();
+    if (cus <= 0) return fail(TANS_EHIP, "vecadd_fused: cannot query the device's CU count");
+    const int64_t blocks = std::min<int64_t>((groups + per_block - 1) / per_block, cus);
     const int n_tiles = (int)(N / kTile);
 #define TANS_LAUNCH_FUSED(S)                                                                      \
     hipLaunchKernelGGL((fused_add_kernel<S, kFusedGroups<S>>), dim3((unsigned)blocks),              \
