@@ -145,6 +145,31 @@ def test_vecadd_fused_vs_raw_and_oracle(R, lut, alphabet, K, N):
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("K,N", [(300037, 16), (270000, 48)])
+def test_vecadd_fused_several_groups_per_wave(R, lut, alphabet, K, N):
+    """The fused kernel runs at most one workgroup per CU (4096 waves on
+    MI355X) and each wave loops over groups w, w + 4096, ...  With K/64 >
+    4096 groups most waves decode two or more groups in turn, the last one
+    partial (K % 64 = 5 and 48), with last tiles of 16 elements (one tile
+    per lane) and 48."""
+    from rans_vectoradd import tans_codec as T
+    _say(f"case: fp8_vecadd_fused_tans K={K} N={N} {alphabet} (several groups per wave)")
+    assert (K + 63) // 64 > 4096
+    exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
+    torch.manual_seed(K + N)
+    fa = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
+    fb = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
+    ca, sa, oa, pa, sma, pf, sp = T.encode(fa, exp_freqs, alphabet=alphabet)
+    cb, sb, ob, pb, smb, _, _ = T.encode(fb, exp_freqs, alphabet=alphabet)
+    tbl = T.build_decode_table(sp.numpy(), pf.numpy())
+    args = [t.cuda() for t in (ca, oa, sa, pa, sma, cb, ob, sb, pb, smb, tbl)]
+    fused = T.untile(R.fp8_vecadd_fused_tans(*args, N).cpu(), K, N)
+    ref = O.vecadd(lut, fa.numpy(), fb.numpy()).reshape(K, N)
+    ok = (fused.numpy() == ref) | O.nan_mask_lut()[fa.numpy(), fb.numpy()]
+    assert ok.all(), f"{(~ok).sum()} bytes differ from the oracle"
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
 @pytest.mark.parametrize("dist", ["gaussian", "laplace"])
 def test_decode_config2_data_2p24(R, alphabet, dist):
     """Config-2 data (N(0, 0.02) and Laplace(0, 0.015), scaled to 448, the
