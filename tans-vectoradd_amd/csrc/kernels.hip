@@ -691,7 +691,9 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
 
 // ---------------------------------------------------------------------
 // Standalone decode: two adjacent groups of one tensor per wave (two
-// independent chains per lane); output [N, K], element-major.
+// independent chains per lane); output [N, K], element-major.  A wave takes
+// group pairs g, g + grid groups, ... in turn (the launcher shrinks the grid
+// to one workgroup per CU for columns of one or two tiles).
 //
 // A tile leaves each lane with 16 bytes of its own column (rows 16t ..
 // 16t + 15).  A 4x4 byte transpose inside each quad of lanes (two DPP swaps
@@ -758,6 +760,7 @@ struct DecodeWave {
     uint32_t* xp;           // this wave's staging rows (LDS)
     int n_tiles;
     int lane;
+    int base;               // tiles this wave finished in earlier groups (pacing)
     bool full;              // both groups have 64 lanes in range (wave-uniform)
     bool lines;             // K % 16 == 0: rows start 16-byte aligned
 
@@ -771,7 +774,7 @@ struct DecodeWave {
         // stored.
         uint32_t ex[C][4];
         dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, C>(ch, tbl, lane, ex);
-        pace(progress, lane, (uint32_t)t, live);
+        pace(progress, lane, (uint32_t)(base + t), live);
         uint32_t w[C][4];
         #pragma unroll
         for (int g = 0; g < C; g++) {
@@ -869,9 +872,10 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     table_fetch<L>(tr, table);
     const int lane = threadIdx.x & (kLanes - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
-    const int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * C;
-    const bool live = g0 * kLanes < K;   // wave-uniform
     const int64_t n_groups = (K + kLanes - 1) / kLanes;
+    const int64_t grid_groups = (int64_t)gridDim.x * kDecWaves * C;   // groups per round
+    int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * C;
+    const bool live = g0 < n_groups;   // wave-uniform
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * C;
     DecodeWave<SPS> w;
     w.progress = &smem.progress;
@@ -882,50 +886,62 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     w.n_tiles = (int)(N / kTile) + (rag ? 1 : 0);
     w.tbl = tbl;
     w.sm_stride = K * 8;
-    w.out_tile = out + g0 * kLanes;
     w.qoff = (uint32_t)(lane & 3) * (uint32_t)K + (uint32_t)(lane >> 2) * 4u;
     quad_selectors(lane, w.sel1, w.sel2);
     w.xp = dsmem.xpose[wave];
     w.lines = K % 16 == 0;
-    bool full = true;
     Seg first[C][kSlots];
     uint16_t st0[C];
     bool act[C];
-    #pragma unroll
-    for (int j = 0; j < C; j++) {
-        // a wave past the last group repeats it with no lanes in range
-        const int64_t g = g0 + j < n_groups ? g0 + j : n_groups - 1;
-        const int64_t k0 = g * kLanes;
-        const int lanes = g0 + j < n_groups ? (K - k0 < kLanes ? (int)(K - k0) : kLanes) : 0;
-        full = full && lanes == kLanes;
-        w.lanes[j] = lanes;
-        const bool active = lane < lanes;
-        const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
-        w.sm_bytes[j] = (uint32_t)lanes * 8u;
-        feed_fetch(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], lane, first[j]);
-        st0[j] = st[k0 + lane_ld];
-        act[j] = active;
-        const char* row = reinterpret_cast<const char*>(sm + k0);
+    // the loads of the groups gbase, gbase + 1
+    auto setup = [&](int64_t gbase) {
+        bool full = true;
+        w.out_tile = out + gbase * kLanes;
         #pragma unroll
-        for (int i = 0; i < kSmAhead; i++) {
-            const int64_t ti = i < w.n_tiles ? i : w.n_tiles - 1;
-            w.sm[j][i] = __builtin_amdgcn_raw_buffer_load_b64(
-                rsrc(row + ti * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+        for (int j = 0; j < C; j++) {
+            // a wave past the last group repeats it with no lanes in range
+            const int64_t g = gbase + j < n_groups ? gbase + j : n_groups - 1;
+            const int64_t k0 = g * kLanes;
+            const int lanes = gbase + j < n_groups ? (K - k0 < kLanes ? (int)(K - k0) : kLanes) : 0;
+            full = full && lanes == kLanes;
+            w.lanes[j] = lanes;
+            const bool active = lane < lanes;
+            const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
+            w.sm_bytes[j] = (uint32_t)lanes * 8u;
+            feed_fetch(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], lane, first[j]);
+            st0[j] = st[k0 + lane_ld];
+            act[j] = active;
+            const char* row = reinterpret_cast<const char*>(sm + k0);
+            #pragma unroll
+            for (int i = 0; i < kSmAhead; i++) {
+                const int64_t ti = i < w.n_tiles ? i : w.n_tiles - 1;
+                w.sm[j][i] = __builtin_amdgcn_raw_buffer_load_b64(
+                    rsrc(row + ti * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+            }
+            const int64_t tn = kSmAhead < w.n_tiles ? kSmAhead : w.n_tiles - 1;
+            w.pf[j] = row + tn * w.sm_stride;
         }
-        const int64_t tn = kSmAhead < w.n_tiles ? kSmAhead : w.n_tiles - 1;
-        w.pf[j] = row + tn * w.sm_stride;
-    }
-    w.full = full;
+        w.full = full;
+    };
+    setup(g0);
     table_store<L>(tbl, tr);
     if (threadIdx.x == 0) smem.progress = 0;
     __syncthreads();
     if (!live) return;
-    #pragma unroll
-    for (int j = 0; j < C; j++) {
-        feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
-        lane_init(w.ch.l[j], act[j], st0[j], L);
+    int done = 0;   // tiles of earlier groups (the pacing count runs on)
+    for (;;) {
+        #pragma unroll
+        for (int j = 0; j < C; j++) {
+            feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
+            lane_init(w.ch.l[j], act[j], st0[j], L);
+        }
+        w.base = done;
+        w.run(rag ? rag : kTile);
+        done += w.n_tiles;
+        g0 += grid_groups;
+        if (g0 >= n_groups) break;
+        setup(g0);
     }
-    w.run(rag ? rag : kTile);
 }
 
 // ---------------------------------------------------------------------
@@ -1358,7 +1374,16 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
     if (K > (int64_t(1) << 30)) return fail(TANS_EINVAL, "decode: more than 2^30 lanes");
     const int64_t groups = (K + kLanes - 1) / kLanes;
     const int64_t per_block = (int64_t)kDecWaves * kDecodeGroups;
-    const int64_t blocks = (groups + per_block - 1) / per_block;
+    int64_t blocks = (groups + per_block - 1) / per_block;
+    // Columns of one or two tiles: one workgroup per CU, the waves loop over
+    // their group pairs (measured at 2^30 elements: 16 per column 923 ->
+    // 616 us).  From 4 tiles on, one workgroup per 32 groups is as fast or
+    // faster (64 per column: 472 vs 468 us; 256: 388 vs 400 us).
+    if ((N + kTile - 1) / kTile <= 2) {
+        const int cus = cu_count();
+        if (cus <= 0) return fail(TANS_EHIP, "decode: cannot query the device's CU count");
+        blocks = std::min<int64_t>(blocks, cus);
+    }
     if (blocks > INT32_MAX) return fail(TANS_EINVAL, "decode: K too large");
 #define TANS_LAUNCH_DECODE(S)                                                                     \
     hipLaunchKernelGGL((decode_kernel<S>), dim3((unsigned)blocks),                               \

@@ -145,6 +145,26 @@ def test_vecadd_fused_vs_raw_and_oracle(R, lut, alphabet, K, N):
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("K,N", [(600001, 18), (1048617, 16)])
+def test_decode_several_group_pairs_per_wave(R, alphabet, K, N):
+    """Columns of one or two tiles run one workgroup per CU (8192 group
+    pairs per round on MI355X) and each wave loops over its pairs: here
+    most waves decode two or more pairs, the last group partial (K % 64 =
+    1 and 41) and, at N = 18, a last tile of 2 elements."""
+    from rans_vectoradd import tans_codec as T
+    _say(f"case: gpu_tans_decode K={K} N={N} {alphabet} (several group pairs per wave)")
+    assert (K + 63) // 64 > 2 * 4096
+    exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
+    torch.manual_seed(K)
+    fp8 = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
+    comp, st, off, part, sm, fr, sp = T.encode(fp8, exp_freqs, alphabet=alphabet)
+    dec = R.gpu_tans_decode(comp.cuda(), off.cuda(), st.cuda(), part.cuda(), sm.cuda(),
+                            sp.cuda(), fr.cuda(), N)
+    got = dec.cpu().t().contiguous()
+    assert torch.equal(got, fp8), f"{(got != fp8).sum().item()} mismatched bytes"
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
 @pytest.mark.parametrize("K,N", [(300037, 16), (270000, 48)])
 def test_vecadd_fused_several_groups_per_wave(R, lut, alphabet, K, N):
     """The fused kernel runs at most one workgroup per CU (4096 waves on
