@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <type_traits>
 
 #include "../../include/tans_amd.h"
 
@@ -45,6 +46,15 @@ int hip_check(hipError_t e, const char* what) {
 }
 
 int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
 
 // Workspace layout: chunks u16 [S][K], words u32 [max_words][K],
 // nwords u32 [K], glen u32 [G].
@@ -87,7 +97,59 @@ __device__ __forceinline__ uint32_t symbol_at(const uint8_t* __restrict__ fp8, i
     }
 }
 
-// enc_tab[s] = freq | start << 16; next[start + rank] = L + slot.
+// One backward encode step of symbol s: emit the low nb bits of x that
+// bring it into [f_s, 2 f_s) as the chunk of step i, then x = L + the slot
+// of s's rank-th occurrence.  enc_tab[s] = freq | start << 16;
+// next[start + rank] = L + slot.
+__device__ __forceinline__ void enc_step(uint32_t s, const uint32_t* tab, const uint16_t* nx,
+                                         uint32_t L, uint32_t& x, bool& bad,
+                                         uint16_t* __restrict__ chunks, int64_t i, int64_t K,
+                                         int64_t k) {
+    const uint32_t e = tab[s];
+    uint32_t f = e & 0xFFFFu;
+    if (f == 0) {   // not encodable: flag it and keep every index in range
+        bad = true;
+        f = 1;
+    }
+    int nb = (31 - __builtin_clz(x)) - (31 - __builtin_clz(f));
+    if ((x >> nb) < f) nb--;
+    chunks[i * K + k] = (uint16_t)((x & ((1u << nb) - 1u)) | ((uint32_t)nb << 12));
+    uint32_t idx = (e >> 16) + (x >> nb) - f;
+    idx = idx < L ? idx : L - 1u;
+    x = nx[idx];
+}
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+constexpr int kEncBlockChunks = 8;   // 16-byte chunks per 128-byte block of a row
+
+// Symbol of step q of a 16-byte chunk: bytes 2q, 2q + 1 (pair) or byte q.
+template <int SPS, int Q>
+__device__ __forceinline__ uint32_t chunk_symbol(const v4u& c) {
+    const uint32_t w = c[Q * SPS / 4];
+    constexpr uint32_t sh = (uint32_t)((Q * SPS) % 4) * 8u;
+    if constexpr (SPS == 2) {
+        return (((w >> (sh + 3)) & 0xFu) << 4) | ((w >> (sh + 11)) & 0xFu);
+    } else {
+        return (w >> (sh + 3)) & 0xFu;
+    }
+}
+
+// Chunks top - 1, top - 2, ... of a row into b[0], b[1], ... (zero below 0).
+__device__ __forceinline__ void load_block(v4u (&b)[kEncBlockChunks], const v4u* rp,
+                                           int64_t top) {
+    #pragma unroll
+    for (int c = 0; c < kEncBlockChunks; c++) {
+        const int64_t j = top - 1 - c;
+        b[c] = j >= 0 ? rp[j] : v4u{0u, 0u, 0u, 0u};   // wave-uniform condition
+    }
+}
+
+// One thread per lane walks its row backwards.  When rows are 16-byte
+// aligned (N % 16 == 0) a lane loads its row 128 bytes at a time and the
+// next 128 bytes while it encodes the current ones: a step then waits on
+// LDS only, not on a global load, and each line of the row is fetched in
+// one go (the lanes' rows are N bytes apart, so a line read piecewise over
+// many steps could leave the cache in between).
 template <int SPS>
 __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     const uint8_t* __restrict__ fp8, int64_t K, int64_t N, const uint32_t* __restrict__ enc_tab,
@@ -106,20 +168,31 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     const int64_t row = k * N;
     uint32_t x = L;
     bool bad = false;
-    for (int64_t i = S - 1; i >= 0; i--) {
-        const uint32_t s = symbol_at<SPS>(fp8, row + i * SPS, K * N);
-        const uint32_t e = tab[s];
-        uint32_t f = e & 0xFFFFu;
-        if (f == 0) {   // not encodable: flag it and keep every index in range
-            bad = true;
-            f = 1;
+    if (N % 16 == 0) {   // kernel-uniform
+        constexpr int kQ = 16 / SPS;   // steps per chunk
+        const v4u* rp = reinterpret_cast<const v4u*>(fp8 + row);
+        const int64_t nch = N / 16;
+        v4u cur[kEncBlockChunks], nxt[kEncBlockChunks];
+        load_block(cur, rp, nch);
+        for (int64_t hi = nch; hi > 0; hi -= kEncBlockChunks) {
+            load_block(nxt, rp, hi - kEncBlockChunks);
+            #pragma unroll
+            for (int c = 0; c < kEncBlockChunks; c++) {
+                const int64_t j = hi - 1 - c;
+                if (j < 0) break;   // wave-uniform
+                static_for<0, kQ>([&](auto Q) {
+                    constexpr int q = kQ - 1 - decltype(Q)::value;
+                    enc_step(chunk_symbol<SPS, q>(cur[c]), tab, nx, L, x, bad, chunks,
+                             j * kQ + q, K, k);
+                });
+            }
+            #pragma unroll
+            for (int c = 0; c < kEncBlockChunks; c++) cur[c] = nxt[c];
         }
-        int nb = (31 - __builtin_clz(x)) - (31 - __builtin_clz(f));
-        if ((x >> nb) < f) nb--;
-        chunks[i * K + k] = (uint16_t)((x & ((1u << nb) - 1u)) | ((uint32_t)nb << 12));
-        uint32_t idx = (e >> 16) + (x >> nb) - f;
-        idx = idx < L ? idx : L - 1u;
-        x = nx[idx];
+    } else {
+        for (int64_t i = S - 1; i >= 0; i--)
+            enc_step(symbol_at<SPS>(fp8, row + i * SPS, K * N), tab, nx, L, x, bad, chunks, i, K,
+                     k);
     }
     states[k] = (uint16_t)x;
     if (bad) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it

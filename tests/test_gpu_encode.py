@@ -34,8 +34,11 @@ def _compare(T, fp8, hist, alphabet):
 @pytest.mark.parametrize("alphabet", ALPHABETS)
 @pytest.mark.parametrize("K,N", [(128, 128), (1024, 128), (10000, 128), (100000, 128),
                                  (64, 2), (65, 18), (200, 130), (3, 1000), (1, 16),
-                                 (127, 4096), (130, 30), (4096, 14)])
+                                 (127, 4096), (130, 30), (4096, 14), (300, 208), (70, 48)])
 def test_gpu_encode_matches_cpu(R, alphabet, K, N):
+    """N % 16 == 0 takes the backward pass that reads rows in 128-byte blocks
+    (whole blocks at N = 128, 4096; a partial last block at 208, 48, 16);
+    the other widths read one step's bytes at a time."""
     from rans_vectoradd import tans_codec as T
     _say(f"case: encode_gpu K={K} N={N} {alphabet}")
     torch.manual_seed(42)
