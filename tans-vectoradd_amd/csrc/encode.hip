@@ -13,9 +13,11 @@
 //   enc_pack_kernel      one wave per group: each lane packs its chunks into
 //                        words [w][K]; the wave replays the refill schedule
 //                        to count the group's stream words (padded to 4)
+//                        and records at which checks each lane takes a word
 //   enc_scan_kernel      exclusive prefix of the group counts -> offsets
-//   enc_interleave_kernel one wave per group: replays the schedule again and
-//                        writes each taken word at offset + handed + rank
+//   enc_interleave_kernel one wave per group: replays the schedule from those
+//                        bits and writes each taken word at offset + handed
+//                        + rank
 //   enc_sm_kernel        sign/mantissa tiles
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -57,20 +59,23 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // Workspace layout: chunks u16 [S][K], words u32 [max_words][K],
-// nwords u32 [K], glen u32 [G].
+// nwords u32 [K], glen u32 [G], takes u32 [ceil(checks / 32)][K] (bit q % 32
+// of word q / 32: the lane takes a word at refill check q).
 struct WsLayout {
-    int64_t chunks, words, nwords, glen, total;
+    int64_t chunks, words, nwords, glen, takes, total;
 };
 
 WsLayout ws_layout(int64_t K, int64_t S, int32_t log2L) {
     const int64_t G = (K + kLanes - 1) / kLanes;
     const int64_t max_words = (S * log2L + 31) / 32 + 1;
+    const int64_t take_words = ((S + 1) / 2 + 31) / 32;
     WsLayout l;
     l.chunks = 0;
     l.words = align256(S * K * 2);
     l.nwords = l.words + align256(max_words * K * 4);
     l.glen = l.nwords + align256(K * 4);
-    l.total = l.glen + align256(G * 4);
+    l.takes = l.glen + align256(G * 4);
+    l.total = l.takes + align256(take_words * K * 4);
     return l;
 }
 
@@ -198,12 +203,18 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     if (bad) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
 }
 
-// The refill schedule, replayed by both forward passes: before step 2q each
-// active lane holding fewer than 24 bits takes the next word (+32 bits), then
-// steps 2q and 2q + 1 consume their nb bits.
+// The refill schedule: before step 2q each active lane holding fewer than
+// 24 bits takes the next word (+32 bits), then steps 2q and 2q + 1 consume
+// their nb bits.  This pass replays it while it packs each lane's chunks
+// into words, and records per check whether the lane takes a word, so
+// enc_interleave_kernel needs only those bits.  Chunks are read 16 steps at
+// a time (a step past S reads as an empty chunk).
+constexpr int kPackChecks = 8;
+
 __global__ __launch_bounds__(kEncBlock) void enc_pack_kernel(
     const uint16_t* __restrict__ chunks, int64_t K, int64_t S, int64_t max_words,
-    uint32_t* __restrict__ words, uint32_t* __restrict__ nwords, uint32_t* __restrict__ glen) {
+    uint32_t* __restrict__ words, uint32_t* __restrict__ nwords, uint32_t* __restrict__ glen,
+    uint32_t* __restrict__ takes) {
     const int lane = threadIdx.x & (kLanes - 1);
     const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) + threadIdx.x / kLanes;
     const int64_t G = (K + kLanes - 1) / kLanes;
@@ -213,29 +224,44 @@ __global__ __launch_bounds__(kEncBlock) void enc_pack_kernel(
     const int64_t kk = active ? k : K - 1;
     uint64_t acc = 0;
     int n = 0;
-    uint32_t nw = 0, taken = 0;
+    uint32_t nw = 0, taken = 0, tw = 0;
     int cnt = 0;
     const int64_t n_checks = (S + 1) / 2;
-    for (int64_t q = 0; q < n_checks; q++) {
-        if (cnt < kRefillBelow) {
-            taken++;
-            cnt += 32;
+    static_assert(32 % kPackChecks == 0, "a batch of checks never straddles a takes word");
+    for (int64_t q0 = 0; q0 < n_checks; q0 += kPackChecks) {
+        uint32_t c[2 * kPackChecks];
+        #pragma unroll
+        for (int u = 0; u < 2 * kPackChecks; u++) {
+            const int64_t t = 2 * q0 + u;
+            c[u] = t < S ? chunks[t * K + kk] : 0u;   // wave-uniform condition
         }
         #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int64_t t = 2 * q + h;
-            if (t >= S) break;
-            const uint32_t c = chunks[t * K + kk];
-            const int nb = (int)(c >> 12);
-            cnt -= nb;
-            acc |= (uint64_t)(c & 0xFFFu) << n;
-            n += nb;
-            if (n >= 32) {
-                if (active && nw < max_words) words[(int64_t)nw * K + k] = (uint32_t)acc;
-                nw++;
-                acc >>= 32;
-                n -= 32;
+        for (int u = 0; u < kPackChecks; u++) {
+            if (q0 + u >= n_checks) break;   // wave-uniform
+            if (cnt < kRefillBelow) {
+                taken++;
+                cnt += 32;
+                tw |= 1u << ((q0 + u) % 32);
             }
+            #pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t ch = c[2 * u + h];
+                const int nb = (int)(ch >> 12);
+                cnt -= nb;
+                acc |= (uint64_t)(ch & 0xFFFu) << n;
+                n += nb;
+                if (n >= 32) {
+                    if (active && nw < max_words) words[(int64_t)nw * K + k] = (uint32_t)acc;
+                    nw++;
+                    acc >>= 32;
+                    n -= 32;
+                }
+            }
+        }
+        const int64_t qe = q0 + kPackChecks;
+        if (qe % 32 == 0 || qe >= n_checks) {   // wave-uniform
+            if (active) takes[(q0 / 32) * K + k] = tw;
+            tw = 0;
         }
     }
     if (n > 0) {
@@ -283,8 +309,12 @@ __global__ __launch_bounds__(kEncBlock) void zero_words_kernel(uint32_t* __restr
     if (i < n) p[i] = 0u;
 }
 
+// Replays the schedule from the take bits of enc_pack_kernel: at each check
+// the lanes taking a word write it at offset + handed + rank (ballot +
+// mbcnt, the order the decoders read), 32 checks per take word with the
+// word loads of 8 checks issued together.
 __global__ __launch_bounds__(kEncBlock) void enc_interleave_kernel(
-    const uint16_t* __restrict__ chunks, int64_t K, int64_t S, int64_t max_words,
+    const uint32_t* __restrict__ takes, int64_t K, int64_t S, int64_t max_words,
     const uint32_t* __restrict__ words, const uint32_t* __restrict__ nwords,
     const int64_t* __restrict__ offsets, uint32_t* __restrict__ comp) {
     const int lane = threadIdx.x & (kLanes - 1);
@@ -293,69 +323,111 @@ __global__ __launch_bounds__(kEncBlock) void enc_interleave_kernel(
     if (g >= G) return;   // wave-uniform
     const int64_t k = g * kLanes + lane;
     const bool active = k < K;
-    const int64_t kk = active ? k : K - 1;
     const uint32_t nw = active ? nwords[k] : 0u;
     const int64_t base = offsets[g];
     const int64_t end = offsets[g + 1];
     int64_t handed = 0;
     uint32_t taken = 0;
-    int cnt = 0;
     const int64_t n_checks = (S + 1) / 2;
-    for (int64_t q = 0; q < n_checks; q++) {
-        const bool need = active && cnt < kRefillBelow;
-        const uint64_t m = __ballot(need);
-        const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-        if (need) {
-            const uint32_t w = (taken < nw && taken < max_words)
-                                   ? words[(int64_t)taken * K + k] : 0u;
-            const int64_t pos = base + handed + rank;
-            if (pos < end) comp[pos] = w;
-            taken++;
-            cnt += 32;
-        }
-        handed += __popcll(m);
-        #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int64_t t = 2 * q + h;
-            if (t >= S) break;
-            cnt -= (int)(chunks[t * K + kk] >> 12);
+    constexpr int kBatch = 8;
+    for (int64_t q0 = 0; q0 < n_checks; q0 += 32) {
+        const uint32_t tw = active ? takes[(q0 / 32) * K + k] : 0u;
+        for (int b = 0; b < 32; b += kBatch) {
+            if (q0 + b >= n_checks) break;   // wave-uniform
+            uint32_t w[kBatch];
+            #pragma unroll
+            for (int u = 0; u < kBatch; u++) {   // this lane's words of the batch
+                const uint32_t t = taken + (uint32_t)__builtin_popcount(tw & ((1u << (b + u)) - 1u) &
+                                                                        ~((1u << b) - 1u));
+                const bool take = (tw >> (b + u)) & 1u;
+                w[u] = (take && t < nw && t < max_words) ? words[(int64_t)t * K + k] : 0u;
+            }
+            #pragma unroll
+            for (int u = 0; u < kBatch; u++) {
+                if (q0 + b + u >= n_checks) break;   // wave-uniform
+                const bool need = (tw >> (b + u)) & 1u;
+                const uint64_t m = __ballot(need);
+                const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+                    (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+                if (need) {
+                    const int64_t pos = base + handed + rank;
+                    if (pos < end) comp[pos] = w[u];
+                }
+                handed += __popcll(m);
+            }
+            taken += (uint32_t)__builtin_popcount(tw & (((b + kBatch) >= 32 ? 0xFFFFFFFFu
+                                                                          : ((1u << (b + kBatch)) - 1u)) &
+                                                        ~((1u << b) - 1u)));
         }
     }
     // zero padding up to the 4-word boundary
     if (base + handed + lane < end) comp[base + handed + lane] = 0u;
 }
 
-// Sign/mantissa tiles: thread (t, k) writes sm[(t K + k) * 8] from bytes
-// [16t, 16t + 16) of lane k (zero past N).
+// Sign/mantissa tiles: sm[(t K + k) * 8] from bytes [16t, 16t + 16) of row
+// k (zero past N).  A workgroup of 4 waves takes 32 rows x 64 tiles: each
+// wave reads 8 rows, one row segment of 1 KiB per instruction (lane = tile),
+// turns each 16 bytes into the tile's two sm words, and stages them in LDS
+// by [tile][row]; after a barrier each wave writes 16 tiles as contiguous
+// 256-byte runs of 32 rows.
+constexpr int kSmRows = 32;                      // rows per workgroup
+constexpr int kSmCols = kLanes;                  // tiles per workgroup
+constexpr int kSmPad = kSmRows + 1;              // LDS row stride (records): 2-way banks at most
+
+__device__ __forceinline__ void sm_words(const uint32_t (&b)[4], uint32_t& w0, uint32_t& w1) {
+    const uint32_t m = 0x87878787u;
+    w0 = (b[0] & m) | __builtin_amdgcn_alignbit(b[1] & m, b[1] & m, 28u);
+    w1 = (b[2] & m) | __builtin_amdgcn_alignbit(b[3] & m, b[3] & m, 28u);
+}
+
 __global__ __launch_bounds__(kEncBlock) void enc_sm_kernel(const uint8_t* __restrict__ fp8,
                                                            int64_t K, int64_t N, int64_t n_tiles,
                                                            uint32_t* __restrict__ sm) {
-    const int64_t i = (int64_t)blockIdx.x * kEncBlock + threadIdx.x;
-    if (i >= n_tiles * K) return;
-    const int64_t t = i / K, k = i % K;
-    const uint8_t* row = fp8 + k * N;
-    uint32_t b[4];
-    if (N % kTile == 0) {   // whole, 16-byte aligned tiles
-        const uint4 v = *reinterpret_cast<const uint4*>(row + t * kTile);
-        b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
-    } else {
-        #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            uint32_t v = 0;
-            #pragma unroll
-            for (int y = 0; y < 4; y++) {
-                const int64_t c = t * kTile + 4 * j + y;
-                if (c < N) v |= (uint32_t)row[c] << (8 * y);
+    static_assert(kEncBlock == 4 * kLanes && kSmRows % 4 == 0, "4 waves, 8 rows each");
+    __shared__ uint2 st[kSmCols * kSmPad];
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int wave = threadIdx.x / kLanes;
+    const int64_t col_blocks = (n_tiles + kSmCols - 1) / kSmCols;
+    const int64_t rb = blockIdx.x / col_blocks, cb = blockIdx.x % col_blocks;
+    const int64_t k0 = rb * kSmRows, t0 = cb * kSmCols;
+    const int64_t t = t0 + lane;   // this lane's tile in the load phase
+    constexpr int kPerWave = kSmRows / 4;
+    #pragma unroll
+    for (int u = 0; u < kPerWave; u++) {
+        const int r = wave * kPerWave + u;
+        const int64_t k = k0 + r;
+        uint32_t b[4] = {0u, 0u, 0u, 0u};
+        if (k < K && t < n_tiles) {
+            const uint8_t* row = fp8 + k * N;
+            if (N % kTile == 0) {   // whole, 16-byte aligned tiles
+                const uint4 v = *reinterpret_cast<const uint4*>(row + t * kTile);
+                b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
+            } else {
+                #pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    #pragma unroll
+                    for (int y = 0; y < 4; y++) {
+                        const int64_t c = t * kTile + 4 * q + y;
+                        if (c < N) b[q] |= (uint32_t)row[c] << (8 * y);
+                    }
+                }
             }
-            b[j] = v;
         }
+        uint32_t w0, w1;
+        sm_words(b, w0, w1);
+        st[lane * kSmPad + r] = uint2{w0, w1};
     }
-    const uint32_t m = 0x87878787u;
-    const uint32_t w0 = (b[0] & m) | __builtin_amdgcn_alignbit(b[1] & m, b[1] & m, 28u);
-    const uint32_t w1 = (b[2] & m) | __builtin_amdgcn_alignbit(b[3] & m, b[3] & m, 28u);
-    sm[2 * i] = w0;
-    sm[2 * i + 1] = w1;
+    __syncthreads();
+    // store phase: each instruction writes two tiles x 32 rows (lane / 32, lane % 32)
+    const int r = lane % kSmRows;
+    const int64_t k = k0 + r;
+    #pragma unroll
+    for (int v = 0; v < kSmCols / 8; v++) {
+        const int tt = (wave * (kSmCols / 8) + v) * 2 + lane / kSmRows;
+        const int64_t tg = t0 + tt;
+        if (k < K && tg < n_tiles)
+            *reinterpret_cast<uint2*>(sm + (tg * K + k) * 2) = st[tt * kSmPad + r];
+    }
 }
 
 }  // namespace
@@ -418,13 +490,13 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
                            states, status);
     if ((rc = hip_check(hipGetLastError(), "enc_backward_kernel launch"))) return rc;
     hipLaunchKernelGGL(enc_pack_kernel, dim3(group_blocks), dim3(kEncBlock), 0, st, chunks, K, S,
-                       max_words, words, nwords, glen);
+                       max_words, words, nwords, glen, reinterpret_cast<uint32_t*>(ws + l.takes));
     if ((rc = hip_check(hipGetLastError(), "enc_pack_kernel launch"))) return rc;
     hipLaunchKernelGGL(enc_scan_kernel, dim3(1), dim3(1024), 0, st, glen, G, offsets);
     if ((rc = hip_check(hipGetLastError(), "enc_scan_kernel launch"))) return rc;
-    hipLaunchKernelGGL(enc_sm_kernel, dim3((unsigned)((n_tiles * K + kEncBlock - 1) / kEncBlock)),
-                       dim3(kEncBlock), 0, st, (const uint8_t*)fp8, K, N, n_tiles,
-                       (uint32_t*)sm);
+    const int64_t sm_blocks = (K + kSmRows - 1) / kSmRows * ((n_tiles + kSmCols - 1) / kSmCols);
+    hipLaunchKernelGGL(enc_sm_kernel, dim3((unsigned)sm_blocks), dim3(kEncBlock), 0, st,
+                       (const uint8_t*)fp8, K, N, n_tiles, (uint32_t*)sm);
     return hip_check(hipGetLastError(), "enc_sm_kernel launch");
 }
 
@@ -448,7 +520,7 @@ int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* work
         const char* ws = static_cast<const char*>(workspace);
         hipLaunchKernelGGL(enc_interleave_kernel,
                            dim3((unsigned)((G + kEncBlock / kLanes - 1) / (kEncBlock / kLanes))),
-                           dim3(kEncBlock), 0, st, reinterpret_cast<const uint16_t*>(ws + l.chunks),
+                           dim3(kEncBlock), 0, st, reinterpret_cast<const uint32_t*>(ws + l.takes),
                            K, S, max_words, reinterpret_cast<const uint32_t*>(ws + l.words),
                            reinterpret_cast<const uint32_t*>(ws + l.nwords), offsets, c32);
         if ((rc = hip_check(hipGetLastError(), "enc_interleave_kernel launch"))) return rc;
