@@ -269,6 +269,42 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
 # GPU encoder (the same bytes as encode(), from FP8 bytes on the device)
 # ---------------------------------------------------------------------------
 
+_ENC_TABLES: dict = {}
+_ENC_TABLES_MAX = 16
+
+
+def _encode_tables(exp_freqs, alphabet: str, dev: torch.device):
+    """(freqs, spread, enc_tab on dev, enc_next on dev) for a histogram.  The
+    quantization costs about a millisecond of host time, so the tables of the
+    last few (histogram, alphabet, device) keys are kept; the numpy arrays
+    are read-only so a caller cannot change a cached entry."""
+    h = np.ascontiguousarray(np.asarray(exp_freqs, dtype=np.float64))
+    key = (alphabet, h.shape, h.tobytes(), str(dev))
+    hit = _ENC_TABLES.get(key)
+    if hit is not None:
+        return hit
+    nsym, L, _ = ALPHABETS[alphabet]
+    log2L = L.bit_length() - 1
+    freqs = symbol_freqs(h, alphabet)
+    spread = build_spread(freqs)
+    enc_tab = np.empty(nsym, dtype=np.uint32)
+    enc_next = np.empty(L, dtype=np.uint16)
+    check(lib.tans_build_encode_table(ctypes.c_void_p(spread.ctypes.data),
+                                      ctypes.c_void_p(freqs.ctypes.data), nsym, log2L,
+                                      ctypes.c_void_p(enc_tab.ctypes.data),
+                                      ctypes.c_void_p(enc_next.ctypes.data)),
+          "encode_gpu")
+    freqs.setflags(write=False)
+    spread.setflags(write=False)
+    with torch.cuda.device(dev):
+        tab_d = torch.from_numpy(enc_tab.view(np.int32)).to(dev)
+        next_d = torch.from_numpy(enc_next.view(np.int16)).to(dev)
+    if len(_ENC_TABLES) >= _ENC_TABLES_MAX:
+        _ENC_TABLES.pop(next(iter(_ENC_TABLES)))
+    _ENC_TABLES[key] = (freqs, spread, tab_d, next_d)
+    return _ENC_TABLES[key]
+
+
 def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair"):
     """encode() on the GPU: FP8 bytes [K, N] (uint8, on a GPU, N even) ->
     the same 7-tuple with the same bytes, as device tensors (freqs and
@@ -290,16 +326,8 @@ def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: s
         exp_freqs = exp_freqs.detach().cpu().float().numpy()
     nsym, L, _ = ALPHABETS[alphabet]
     log2L = L.bit_length() - 1
-    freqs = symbol_freqs(exp_freqs, alphabet)
-    spread = build_spread(freqs)
-    enc_tab = np.empty(nsym, dtype=np.uint32)
-    enc_next = np.empty(L, dtype=np.uint16)
-    check(lib.tans_build_encode_table(ctypes.c_void_p(spread.ctypes.data),
-                                      ctypes.c_void_p(freqs.ctypes.data), nsym, log2L,
-                                      ctypes.c_void_p(enc_tab.ctypes.data),
-                                      ctypes.c_void_p(enc_next.ctypes.data)),
-          "encode_gpu")
     dev = fp8_bytes.device
+    freqs, spread, tab_d, next_d = _encode_tables(exp_freqs, alphabet, dev)
     x = fp8_bytes.contiguous()
     if x.data_ptr() % 16:            # the kernels read 4- and 16-byte words
         x = x.clone()
@@ -312,8 +340,6 @@ def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: s
         states = torch.empty(K, dtype=torch.uint16, device=dev)
         sm = torch.empty(((N + 15) // 16, K, 8), dtype=torch.uint8, device=dev)
         status = torch.zeros(1, dtype=torch.int32, device=dev)
-        tab_d = torch.from_numpy(enc_tab.view(np.int32)).to(dev)
-        next_d = torch.from_numpy(enc_next.view(np.int16)).to(dev)
         stream = torch.cuda.current_stream(dev).cuda_stream
         check(lib.tans_gpu_encode_begin(x.data_ptr(), K, N, tab_d.data_ptr(), next_d.data_ptr(),
                                         log2L, ws.data_ptr(), ws.numel(), offsets.data_ptr(),
@@ -326,8 +352,8 @@ def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: s
         check(lib.tans_gpu_encode_finish(K, N, log2L, ws.data_ptr(), offsets.data_ptr(),
                                          comp.data_ptr(), comp.numel(), stream), "encode_gpu")
     partial = torch.empty(0, dtype=torch.uint8, device=dev)
-    return (comp, states, offsets, partial, sm, torch.from_numpy(freqs).to(dev),
-            torch.from_numpy(spread).to(dev))
+    return (comp, states, offsets, partial, sm, torch.from_numpy(freqs.copy()).to(dev),
+            torch.from_numpy(spread.copy()).to(dev))
 
 
 @dataclasses.dataclass
