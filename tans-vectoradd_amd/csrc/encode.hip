@@ -102,24 +102,45 @@ __device__ __forceinline__ uint32_t symbol_at(const uint8_t* __restrict__ fp8, i
     }
 }
 
-// One backward encode step of symbol s: emit the low nb bits of x that
-// bring it into [f_s, 2 f_s) as the chunk of step i, then x = L + the slot
-// of s's rank-th occurrence.  enc_tab[s] = freq | start << 16;
-// next[start + rank] = L + slot.
-__device__ __forceinline__ void enc_step(uint32_t s, const uint32_t* tab, const uint16_t* nx,
-                                         uint32_t L, uint32_t& x, bool& bad,
-                                         uint16_t* __restrict__ chunks, int64_t i, int64_t K,
-                                         int64_t k) {
-    const uint32_t e = tab[s];
+// Per-symbol step constants (the FSE formulation of the same construction).
+// For x in [L, 2L) the step emits the nb low bits of x with x >> nb in
+// [f, 2f): nb = (x + dnb) >> 16 with maxb = log2L - floor(log2(f - 1))
+// (log2L for f = 1) and dnb = (maxb << 16) - (f << maxb); then x = next[idx]
+// with idx = start + (x >> nb) - f = (x >> nb) + dfind.  This gives the same
+// nb as floor(log2 x) - floor(log2 f), less one when x >> nb < f, for every
+// f in [1, L] and x in [L, 2L).  A symbol of frequency 0 is encoded as if
+// f = 1 (every index stays in range) and flagged in bit 31 of dnb.
+__device__ __forceinline__ uint2 enc_consts(uint32_t e, int log2L) {
     uint32_t f = e & 0xFFFFu;
-    if (f == 0) {   // not encodable: flag it and keep every index in range
-        bad = true;
-        f = 1;
-    }
-    int nb = (31 - __builtin_clz(x)) - (31 - __builtin_clz(f));
-    if ((x >> nb) < f) nb--;
-    chunks[i * K + k] = (uint16_t)((x & ((1u << nb) - 1u)) | ((uint32_t)nb << 12));
-    uint32_t idx = (e >> 16) + (x >> nb) - f;
+    const uint32_t start = e >> 16;
+    const uint32_t bad = f == 0 ? 1u : 0u;
+    if (f == 0) f = 1;
+    const uint32_t maxb = f == 1 ? (uint32_t)log2L
+                                 : (uint32_t)log2L - (31u - (uint32_t)__builtin_clz(f - 1u));
+    const uint32_t dnb = (maxb << 16) - (f << maxb);
+    return uint2{dnb | (bad << 31), start - f};
+}
+
+// One backward encode step of symbol s: emit the chunk of step i (value in
+// bits 11:0, nb in bits 15:12), then x = L + the slot of s's rank-th
+// occurrence.  bad collects the flags of the symbols seen.
+// The chunk goes to row i of chunks [S][K] through a buffer resource on that
+// row (a scalar base; the lane's offset k * 2 is fixed), so the store costs
+// no per-step address arithmetic.
+__device__ __forceinline__ void enc_step(uint32_t s, const uint2* tab, const uint16_t* nx,
+                                         uint32_t L, uint32_t& x, uint32_t& bad,
+                                         uint16_t* __restrict__ chunks, int64_t i, int64_t K,
+                                         uint32_t koff) {
+    const uint2 e = tab[s];
+    bad |= e.x;
+    const uint32_t nb = __builtin_amdgcn_ubfe(x + e.x, 16u, 5u);
+    const uint32_t ch = __builtin_amdgcn_ubfe(x, 0u, nb) | (nb << 12);
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)ch,
+                                          __builtin_amdgcn_make_buffer_rsrc(chunks + i * K, (short)0,
+                                                                            (int)(K * 2),
+                                                                            0x00020000),
+                                          koff, 0, 0);
+    uint32_t idx = (x >> nb) + e.y;
     idx = idx < L ? idx : L - 1u;
     x = nx[idx];
 }
@@ -161,10 +182,10 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     const uint16_t* __restrict__ next, int log2L, uint16_t* __restrict__ chunks,
     uint16_t* __restrict__ states, int* __restrict__ status) {
     constexpr int NSYM = SPS == 2 ? 256 : 16;
-    __shared__ uint32_t tab[NSYM];
+    __shared__ uint2 tab[NSYM];
     __shared__ uint16_t nx[1 << TANS_PAIR_LOG2L];
     const uint32_t L = 1u << log2L;
-    for (int i = threadIdx.x; i < NSYM; i += blockDim.x) tab[i] = enc_tab[i];
+    for (int i = threadIdx.x; i < NSYM; i += blockDim.x) tab[i] = enc_consts(enc_tab[i], log2L);
     for (uint32_t i = threadIdx.x; i < L; i += blockDim.x) nx[i] = next[i];
     __syncthreads();
     const int64_t k = (int64_t)blockIdx.x * kEncBlock + threadIdx.x;
@@ -172,7 +193,8 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     const int64_t S = N / SPS;
     const int64_t row = k * N;
     uint32_t x = L;
-    bool bad = false;
+    uint32_t bad = 0;   // bit 31: a symbol of frequency 0
+    const uint32_t koff = (uint32_t)k * 2u;   // K <= INT32_MAX (checked by the launcher)
     if (N % 16 == 0) {   // kernel-uniform
         constexpr int kQ = 16 / SPS;   // steps per chunk
         const v4u* rp = reinterpret_cast<const v4u*>(fp8 + row);
@@ -188,7 +210,7 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
                 static_for<0, kQ>([&](auto Q) {
                     constexpr int q = kQ - 1 - decltype(Q)::value;
                     enc_step(chunk_symbol<SPS, q>(cur[c]), tab, nx, L, x, bad, chunks,
-                             j * kQ + q, K, k);
+                             j * kQ + q, K, koff);
                 });
             }
             #pragma unroll
@@ -197,10 +219,10 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     } else {
         for (int64_t i = S - 1; i >= 0; i--)
             enc_step(symbol_at<SPS>(fp8, row + i * SPS, K * N), tab, nx, L, x, bad, chunks, i, K,
-                     k);
+                     koff);
     }
     states[k] = (uint16_t)x;
-    if (bad) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
+    if (bad >> 31) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
 }
 
 // The refill schedule: before step 2q each active lane holding fewer than
