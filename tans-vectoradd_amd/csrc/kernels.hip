@@ -577,11 +577,14 @@ struct FusedWave {
                                                    (uint32_t)lane * 16u, 0, kNT);
             out_cur[g] += out_stride;
         }
-        // sign/mantissa of tile min(t + kSmAhead, n_tiles - 1): the loads are unconditional
+        // sign/mantissa of tile t + kSmAhead.  The loads are unconditional (the
+        // wait counts stay exact); past the last tile they have an empty bound
+        // and read nothing.
+        const bool sm_next = t + kSmAhead < n_tiles;   // wave-uniform
         #pragma unroll
         for (int c = 0; c < C; c++)
-            sm[c][P] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(pf[c], sm_bytes[c / 2]),
-                                                            (uint32_t)lane * 8u, 0, kNT);
+            sm[c][P] = __builtin_amdgcn_raw_buffer_load_b64(
+                rsrc(pf[c], sm_next ? sm_bytes[c / 2] : 0u), (uint32_t)lane * 8u, 0, kNT);
         if (t + kSmAhead + 1 < n_tiles) {
             #pragma unroll
             for (int c = 0; c < C; c++) pf[c] += sm_stride;
@@ -651,7 +654,8 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
                 for (int i = 0; i < kSmAhead; i++) {
                     const int64_t ti = i < n_tiles ? i : n_tiles - 1;
                     w.sm[c][i] = __builtin_amdgcn_raw_buffer_load_b64(
-                        rsrc(rows[s] + ti * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+                        rsrc(rows[s] + ti * w.sm_stride, i < n_tiles ? w.sm_bytes[j] : 0u),
+                        (uint32_t)lane * 8u, 0, kNT);
                 }
                 const int64_t tn = kSmAhead < n_tiles ? kSmAhead : n_tiles - 1;
                 w.pf[c] = rows[s] + tn * w.sm_stride;
@@ -833,7 +837,10 @@ struct DecodeWave {
             }
         }
         out_tile += kTile * K;
-        // sign/mantissa of tile min(t + kSmAhead, n_tiles - 1): the loads are unconditional
+        // sign/mantissa of tile min(t + kSmAhead, n_tiles - 1): the loads are
+        // unconditional and, unlike FusedWave::tile, keep their bound past the
+        // last tile (a select there costs this kernel two SGPRs, which it
+        // spills into the tile loop)
         #pragma unroll
         for (int g = 0; g < C; g++)
             sm[g][P] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(pf[g], sm_bytes[g]),
@@ -916,7 +923,8 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
             for (int i = 0; i < kSmAhead; i++) {
                 const int64_t ti = i < w.n_tiles ? i : w.n_tiles - 1;
                 w.sm[j][i] = __builtin_amdgcn_raw_buffer_load_b64(
-                    rsrc(row + ti * w.sm_stride, w.sm_bytes[j]), (uint32_t)lane * 8u, 0, kNT);
+                    rsrc(row + ti * w.sm_stride, i < w.n_tiles ? w.sm_bytes[j] : 0u),
+                    (uint32_t)lane * 8u, 0, kNT);
             }
             const int64_t tn = kSmAhead < w.n_tiles ? kSmAhead : w.n_tiles - 1;
             w.pf[j] = row + tn * w.sm_stride;
@@ -1029,10 +1037,13 @@ struct GemmWave {
                 acc[c][b] = a;
             }
         }
+        // sign/mantissa of tile t + kSmAhead (an empty bound past the last tile,
+        // as in FusedWave::tile)
+        const bool sm_next = t + kSmAhead < n_tiles;   // wave-uniform
         #pragma unroll
         for (int c = 0; c < C; c++)
-            sm[c][P] = __builtin_amdgcn_raw_buffer_load_b64(rsrc(pf[c], sm_bytes),
-                                                            (uint32_t)lane * 8u, 0, kNT);
+            sm[c][P] = __builtin_amdgcn_raw_buffer_load_b64(
+                rsrc(pf[c], sm_next ? sm_bytes : 0u), (uint32_t)lane * 8u, 0, kNT);
         if (t + kSmAhead + 1 < n_tiles) {
             #pragma unroll
             for (int c = 0; c < C; c++) pf[c] += sm_stride;
@@ -1118,7 +1129,8 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
         for (int i = 0; i < kSmAhead; i++) {
             const int64_t ti = i < w.n_tiles ? i : w.n_tiles - 1;
             w.sm[j][i] = __builtin_amdgcn_raw_buffer_load_b64(
-                rsrc(row + ti * w.sm_stride, w.sm_bytes), (uint32_t)lane * 8u, 0, kNT);
+                rsrc(row + ti * w.sm_stride, i < w.n_tiles ? w.sm_bytes : 0u), (uint32_t)lane * 8u,
+                0, kNT);
         }
         const int64_t tn = kSmAhead < w.n_tiles ? kSmAhead : w.n_tiles - 1;
         w.pf[j] = row + tn * w.sm_stride;
