@@ -21,8 +21,9 @@ Prints ONE JSON line (progress goes to stderr):
                 bounded sample of the same workload
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
-    python bench.py --profile fused|raw|memcpy|decode [--alphabet pair|nibble] --steps 5
-                                  # one kernel only, for rocprofv3
+    python bench.py --profile fused|raw|memcpy|decode|gemv|gemv_raw|encode
+                    [--alphabet pair|nibble] --steps 5
+                                  # one kernel (or the encoder's passes) only, for rocprofv3
 """
 from __future__ import annotations
 
@@ -65,7 +66,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-gemm", action="store_true", help="skip configs 3-4 (decode-GEMV/GEMM)")
     p.add_argument("--alphabet", choices=("pair", "nibble"), default="pair",
                    help="alphabet of --profile fused/decode")
-    p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode", "gemv", "gemv_raw"),
+    p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode", "gemv", "gemv_raw",
+                                         "encode"),
                    help="only launch this kernel --steps times (for rocprofv3)")
     return p.parse_args()
 
@@ -503,6 +505,12 @@ def profile_only(args) -> None:
             fn = lambda: R.fp8_gemm_fused_tans(m, tbl, x, sc)   # noqa: E731
         else:
             fn = lambda: R.fp8_gemm_raw(w, x, sc)               # noqa: E731
+    elif args.profile == "encode":   # encode_gpu of one config-1 vector (2^29, 1024 per lane)
+        from rans_vectoradd import data as D
+        q, _ = D.gaussian_fp8_bytes(N_ELEMS, seed=args.seed, device="cuda")
+        x = q.reshape(N_ELEMS // HEADLINE_LANE, HEADLINE_LANE)
+        hist = D.exp_histogram(q).cpu()
+        fn = lambda: T.encode_gpu(x, hist, alphabet=args.alphabet)   # noqa: E731
     elif args.profile == "decode":   # config 2: 2^30 Gaussian elements, 1024 per lane
         from rans_vectoradd import data as D
         K = DECODE_ELEMS // HEADLINE_LANE
