@@ -1171,8 +1171,12 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
 // y[b][r] = bf16(scale * sum over s of ws[s][b][r]).  A block of 4 waves
 // takes 64 consecutive outputs of one batch row: wave w sums segments
 // s = w, w + 4, ... in ascending order (coalesced 256-byte loads), and the
-// four sums are added in wave order, so the result is deterministic.
+// four sums are added in wave order, so the result is deterministic.  A
+// wave issues the loads of kFinBatch segments before it adds any of them,
+// so a call pays one memory round trip per kFinBatch segments instead of
+// one per segment.
 constexpr int kFinWaves = 4;
+constexpr int kFinBatch = 8;
 
 __global__ __launch_bounds__(kFinWaves * kLanes) void gemm_finalize_kernel(
     const float* __restrict__ ws, int S, int NB, int64_t Rp, int64_t R, float scale,
@@ -1184,7 +1188,17 @@ __global__ __launch_bounds__(kFinWaves * kLanes) void gemm_finalize_kernel(
     const int64_t b = blockIdx.x / blocks_per_b;
     const int64_t r = (blockIdx.x % blocks_per_b) * kLanes + lane;   // < Rp: Rp is a multiple of 64
     float a = 0.0f;
-    for (int s = wave; s < S; s += kFinWaves) a += ws[((int64_t)s * NB + b) * Rp + r];
+    for (int s0 = wave; s0 < S; s0 += kFinWaves * kFinBatch) {
+        float v[kFinBatch];
+        #pragma unroll
+        for (int i = 0; i < kFinBatch; i++) {
+            const int s = s0 + i * kFinWaves < S ? s0 + i * kFinWaves : S - 1;   // in bounds
+            v[i] = ws[((int64_t)s * NB + b) * Rp + r];
+        }
+        #pragma unroll
+        for (int i = 0; i < kFinBatch; i++)
+            if (s0 + i * kFinWaves < S) a += v[i];
+    }
     part[wave][lane] = a;
     __syncthreads();
     if (wave == 0 && r < R) {
