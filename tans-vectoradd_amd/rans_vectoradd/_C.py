@@ -142,6 +142,8 @@ def gpu_tans_decode(compressed: torch.Tensor, offsets: torch.Tensor, states: tor
     _require((nsym, log2L) in ((256, TANS_PAIR_LOG2L), (16, TANS_NIBBLE_LOG2L)),
              "freqs must hold 256 pair or 16 nibble frequencies matching the spread size")
     dev = compressed.device
+    for t in (offsets, states, sign_mantissa, spread, freqs):
+        _require(t.device == dev, "all tensors must be on one device")
     out = torch.empty((N, K), dtype=torch.uint8, device=dev)
     if K == 0 or N == 0:
         return out
