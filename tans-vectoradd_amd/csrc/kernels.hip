@@ -28,14 +28,14 @@
 // mbcnt for each lane's rank and one ds_read_b32 from the wave's LDS ring.
 // The ring holds kSlots segments of 256 words (one 16-byte load per lane)
 // plus a 64-word mirror of its first words, so a wave's 64 consecutive reads
-// never wrap.  Each stage issues one segment load per stream through a
-// buffer resource whose bound is the room left in the stream (an idle stage
-// loads with an empty bound, which reads nothing), and writes it into the
-// ring kDelay stages later.  A stage is four refill checks, so at most 256
-// words are handed out per stage, and kSlots = kDelay + 2 guarantees every
-// segment is in the ring before a lane asks for it.  All vector-memory
-// instructions run in a fixed order, so the compiler's wait counts stay
-// exact and no stage waits for a full memory round trip.
+// never wrap.  A stage issues at most one segment load per stream, through
+// a buffer resource whose bound is the room left in the stream, once the
+// segment's ring slot is free.  The loaded segment stays in registers and is
+// written into the ring no earlier than the next stage and no later than
+// the stage in which a lane could first take one of its words.  A stage is
+// four refill checks, so at most 256 words are handed out per stage, and
+// kSlots = kDelay + 2 slots guarantee that a fetched segment starts more
+// than a stage's worth of words ahead of the lanes.
 //
 // FP8 bytes are rebuilt four at a time: the table carries each exponent
 // pre-shifted to bits 6:3 of a byte, a v_perm gathers four of them and one
@@ -249,7 +249,7 @@ constexpr int kRefillBelow = 24;           // a lane with fewer unread bits take
 typedef v4u Seg;                           // one segment: 16 bytes per lane
 constexpr int kSegWords = 4 * kLanes;
 constexpr int kChecksPerStage = 4;         // a stage is 4 refill checks (8 steps)
-constexpr int kDelay = 1;                  // stages from a segment load to its ring write
+constexpr int kDelay = 1;                  // stages from a segment load to its earliest ring write
 constexpr int kSlots = kDelay + 2;
 constexpr int kRingWords = kSlots * kSegWords;
 constexpr int kMirrorWords = kLanes;
@@ -258,9 +258,9 @@ constexpr int kDecWaves = 16;              // waves per workgroup
 constexpr int kSmAhead = 4;                // sign/mantissa rows are loaded this many tiles ahead
 constexpr int kDecBlock = kDecWaves * kLanes;
 // At most kChecksPerStage * 64 words are handed out per stage.  A segment is
-// fetched once the one kSlots earlier in its slot is consumed; it is written
-// kDelay stages later and first read no earlier than
-// (kSlots - 1) * kSegWords - kChecksPerStage * 64 words after the fetch
+// fetched once the one kSlots earlier in its slot is consumed; it can be
+// written kDelay stages later at the earliest and is first read no earlier
+// than (kSlots - 1) * kSegWords - kChecksPerStage * 64 words after the fetch
 // decision.
 static_assert((kSlots - 1) * kSegWords >= (kDelay + 1) * kChecksPerStage * kLanes,
               "ring too small for the delay");
@@ -274,7 +274,8 @@ struct Feed {
     uint32_t next_slot;     // ring slot of `next`
     uint32_t handed;        // words handed to lanes so far
     uint32_t ring_b;        // byte offset in the ring of word `handed`
-    int32_t dest[kDelay];   // ring slot of the fetch issued at each stage, -1 if idle
+    int32_t dest[kDelay];   // ring slot of the pending (loaded, unwritten) segment, -1 if none
+    uint32_t pend_word;     // stream word index of the pending segment's first word
     uint32_t* ring;         // this wave's ring for this stream (LDS)
 };
 
@@ -343,22 +344,35 @@ __device__ __forceinline__ void feed_commit(Feed& f, int lane, const Seg (&first
         f.dest[i] = -1;
         pend[i] = Seg{0u, 0u, 0u, 0u};
     }
+    f.pend_word = 0;
 }
 
-// Start of stage ST: write the fetch issued kDelay stages ago, then issue
-// this stage's fetch.  The next segment is fetched when it exists and its
-// slot is free (the segment kSlots earlier is consumed); otherwise the load
-// has an empty bound and reads nothing.
+// Start of a stage.  The next segment is fetched when it exists and its
+// slot is free (the segment kSlots earlier is consumed).  A loaded segment
+// stays pending in registers until the ring needs it: it is written when
+// the lanes could reach its first word during this stage (they take at
+// most kChecksPerStage * 64 words per stage) or when the next fetch needs
+// its registers.  Writing it only then, not one stage after its load,
+// leaves its load several stages to arrive when the stream is consumed
+// slowly.
 template <int ST>
 __device__ __forceinline__ void feed_stage(Feed& f, Seg (&pend)[kDelay], int lane) {
-    const int32_t d = f.dest[ST];
-    if (d >= 0) write_seg(f.ring, d, pend[ST], lane);
+    static_assert(kDelay == 1 && ST == 0, "one pending segment per stream");
+    const int32_t d = f.dest[0];
     const uint32_t free_to = f.handed + (uint32_t)((kSlots - 1) * kSegWords) + 1;
     const uint32_t lim = f.len < free_to ? f.len : free_to;
     const bool fetch = f.next_word < lim;
-    pend[ST] = fetch_seg(f, fetch, lane);
-    f.dest[ST] = fetch ? (int32_t)f.next_slot : -1;
-    if (fetch) feed_advance(f);
+    const bool due = f.pend_word < f.handed + (uint32_t)(kChecksPerStage * kLanes);
+    if (d >= 0 && (fetch || due)) {
+        write_seg(f.ring, d, pend[0], lane);
+        f.dest[0] = -1;
+    }
+    if (fetch) {
+        pend[0] = fetch_seg(f, true, lane);
+        f.dest[0] = (int32_t)f.next_slot;
+        f.pend_word = f.next_word;
+        feed_advance(f);
+    }
 }
 
 // Refill check: lanes with fewer than 24 unread bits take the next words of
