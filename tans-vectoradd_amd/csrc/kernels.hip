@@ -274,7 +274,7 @@ struct Feed {
     uint32_t next_slot;     // ring slot of `next`
     uint32_t handed;        // words handed to lanes so far
     uint32_t ring_b;        // byte offset in the ring of word `handed`
-    int32_t dest[kDelay];   // ring slot of the pending (loaded, unwritten) segment, -1 if none
+    int32_t dest;           // ring slot of the pending (loaded, unwritten) segment, -1 if none
     uint32_t pend_word;     // stream word index of the pending segment's first word
     uint32_t* ring;         // this wave's ring for this stream (LDS)
 };
@@ -336,14 +336,11 @@ __device__ __forceinline__ void feed_fetch(Feed& f, const uint32_t* comp, int64_
 }
 
 __device__ __forceinline__ void feed_commit(Feed& f, int lane, const Seg (&first)[kSlots],
-                                            Seg (&pend)[kDelay]) {
+                                            Seg& pend) {
     #pragma unroll
     for (int i = 0; i < kSlots; i++) write_seg(f.ring, i, first[i], lane);
-    #pragma unroll
-    for (int i = 0; i < kDelay; i++) {
-        f.dest[i] = -1;
-        pend[i] = Seg{0u, 0u, 0u, 0u};
-    }
+    f.dest = -1;
+    pend = Seg{0u, 0u, 0u, 0u};
     f.pend_word = 0;
 }
 
@@ -355,21 +352,20 @@ __device__ __forceinline__ void feed_commit(Feed& f, int lane, const Seg (&first
 // its registers.  Writing it only then, not one stage after its load,
 // leaves its load several stages to arrive when the stream is consumed
 // slowly.
-template <int ST>
-__device__ __forceinline__ void feed_stage(Feed& f, Seg (&pend)[kDelay], int lane) {
-    static_assert(kDelay == 1 && ST == 0, "one pending segment per stream");
-    const int32_t d = f.dest[0];
+__device__ __forceinline__ void feed_stage(Feed& f, Seg& pend, int lane) {
+    static_assert(kDelay == 1, "one pending segment per stream");
+    const int32_t d = f.dest;
     const uint32_t free_to = f.handed + (uint32_t)((kSlots - 1) * kSegWords) + 1;
     const uint32_t lim = f.len < free_to ? f.len : free_to;
     const bool fetch = f.next_word < lim;
     const bool due = f.pend_word < f.handed + (uint32_t)(kChecksPerStage * kLanes);
     if (d >= 0 && (fetch || due)) {
-        write_seg(f.ring, d, pend[0], lane);
-        f.dest[0] = -1;
+        write_seg(f.ring, d, pend, lane);
+        f.dest = -1;
     }
     if (fetch) {
-        pend[0] = fetch_seg(f, true, lane);
-        f.dest[0] = (int32_t)f.next_slot;
+        pend = fetch_seg(f, true, lane);
+        f.dest = (int32_t)f.next_slot;
         f.pend_word = f.next_word;
         feed_advance(f);
     }
@@ -510,19 +506,18 @@ template <int C>
 struct Chains {
     Feed f[C];
     Lane l[C];
-    Seg p[C][kDelay];
+    Seg p[C];   // each chain's pending segment
 };
 
 // Decode the 16 elements of one tile of every chain into exponent words
-// ex[c][4] (4 elements each).  ST0 is the pipeline stage of the tile's first
-// stage.
-template <int SPS, int ST0, int C>
+// ex[c][4] (4 elements each).
+template <int SPS, int C>
 __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ tbl, int lane,
                                          uint32_t (&ex)[C][4]) {
     static_for<0, Alpha<SPS>::kStagesPerTile>([&](auto H) {
         constexpr int h = decltype(H)::value;
         #pragma unroll
-        for (int c = 0; c < C; c++) feed_stage<(ST0 + h) % kDelay>(ch.f[c], ch.p[c], lane);
+        for (int c = 0; c < C; c++) feed_stage(ch.f[c], ch.p[c], lane);
         uint32_t e[C][8];
         #pragma unroll
         for (int q = 0; q < kChecksPerStage; q++) {
@@ -575,7 +570,7 @@ struct FusedWave {
     template <int P>
     __device__ __forceinline__ void tile(int t) {
         uint32_t ex[C][4];
-        dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, C>(ch, tbl, lane, ex);
+        dec_tile<SPS, C>(ch, tbl, lane, ex);
         pace(progress, lane, (uint32_t)(base + t), live);
         #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -791,7 +786,7 @@ struct DecodeWave {
         // and stay inside the table and the ring, and their bytes are not
         // stored.
         uint32_t ex[C][4];
-        dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, C>(ch, tbl, lane, ex);
+        dec_tile<SPS, C>(ch, tbl, lane, ex);
         pace(progress, lane, (uint32_t)(base + t), live);
         uint32_t w[C][4];
         #pragma unroll
@@ -1017,7 +1012,7 @@ struct GemmWave {
         // a ragged last tile is decoded in full (see DecodeWave::tile) and
         // its bytes past n are zeroed before they are used
         uint32_t ex[C][4];
-        dec_tile<SPS, (P * Alpha<SPS>::kStagesPerTile) % kDelay, C>(ch, tbl, lane, ex);
+        dec_tile<SPS, C>(ch, tbl, lane, ex);
         pace(progress, lane, (uint32_t)t, live);
         v2bf wb[C][8];   // bf16 pairs: elements (2m, 2m + 1) of the tile
         #pragma unroll
