@@ -543,8 +543,9 @@ def profile_only(args) -> None:
 def main() -> None:
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: the path has no cross-GPU "
-                                   "step (see DESIGN.md on sharding); run with --gpus 1",
+        print(json.dumps({"error": "this build measures one GPU: vecadd and decode shard by "
+                                   "whole 64-lane groups with no cross-GPU step, so one GPU's "
+                                   "share is the measured kernel; run with --gpus 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.profile:
