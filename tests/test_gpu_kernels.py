@@ -259,3 +259,45 @@ def test_streams_consumed_near_the_feed_limit(R, lut, alphabet):
     ref = O.vecadd(lut, fa.numpy(), fb.numpy()).reshape(K, N)
     ok = (fused.numpy() == ref) | O.nan_mask_lut()[fa.numpy(), fb.numpy()]
     assert ok.all()
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
+def test_decoders_replay_in_a_hip_graph(R, alphabet):
+    """The fused add and the standalone decode (with its device table build)
+    captured in one HIP graph: every replay, with eager launches and host
+    synchronisations between replays, gives the eager results."""
+    from rans_vectoradd import tans_codec as T
+    _say(f"case: fused add + decode in a HIP graph, {alphabet}")
+    K, N = 2048, 128
+    exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
+    torch.manual_seed(3)
+    fa = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
+    fb = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
+    ea = [x.cuda() for x in T.encode(fa, exp_freqs, tile=8, alphabet=alphabet)]
+    eb = [x.cuda() for x in T.encode(fb, exp_freqs, tile=8, alphabet=alphabet)]
+    tbl = T.build_decode_table(ea[6].cpu().numpy(), ea[5].cpu().numpy()).cuda()
+    order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
+    fused_args = [*[ea[i] for i in order], *[eb[i] for i in order], tbl, N]
+    dec_args = [ea[0], ea[2], ea[1], ea[3], ea[4], ea[6], ea[5], N]
+
+    def step():
+        return R.fp8_vecadd_fused_tans(*fused_args), R.gpu_tans_decode(*dec_args)
+
+    eager_sum, eager_dec = step()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):   # warm-up off the default stream before capture
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        g_sum, g_dec = step()
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g_sum, eager_sum), f"replay {i}: fused add differs"
+        assert torch.equal(g_dec, eager_dec), f"replay {i}: decode differs"
+        step()                      # eager work between replays
+        torch.cuda.synchronize()
+    assert torch.equal(eager_dec.cpu().t().contiguous(), fa)
