@@ -53,7 +53,7 @@ enum {
     TANS_OK = 0,
     TANS_EINVAL = -1,     /* bad argument (shape, size, null pointer)      */
     TANS_ENOMEM = -2,     /* host allocation failed                          */
-    TANS_ESYMBOL = -3,    /* data holds a symbol whose frequency is 0         */
+    TANS_ESYMBOL = -3,    /* a symbol outside the alphabet or of frequency 0  */
     TANS_ETABLE = -4,     /* freqs / spread inconsistent                     */
     TANS_EHIP = -5        /* a HIP runtime call failed                       */
 };

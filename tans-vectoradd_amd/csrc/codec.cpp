@@ -80,15 +80,17 @@ int build_enc_tables(const int32_t* freqs, int32_t nsym, const int32_t* spread,
 // Encode one lane of S symbols.  chunk[i] receives step i's bits (low 16)
 // and nb (bits 16+).  words receives the decode-order bitstream, LSB first
 // (room for ceil(S*log2L/32)+1 words).  Returns the word count, or -1 if a
-// symbol has frequency 0.
+// symbol lies outside the alphabet or has frequency 0.
 int64_t encode_lane(const uint8_t* sym, int64_t S, const EncTables& t, uint32_t L,
                     uint32_t* chunk, uint32_t* words, uint32_t* x0) {
     uint32_t x = L;
     const uint32_t* freq = t.freq.data();
     const uint32_t* start = t.start.data();
     const uint32_t* next = t.next.data();
+    const uint32_t nsym = (uint32_t)t.freq.size();
     for (int64_t i = S - 1; i >= 0; i--) {
         const uint32_t s = sym[i];
+        if (s >= nsym) return -1;
         const uint32_t f = freq[s];
         if (f == 0) return -1;
         // nb such that (x >> nb) lies in [f, 2f)
@@ -270,7 +272,7 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
     }
     if (bad_symbol) {
         delete h;
-        return fail(TANS_ESYMBOL, "encode: data holds a symbol whose frequency is 0");
+        return fail(TANS_ESYMBOL, "encode: data holds a symbol outside the alphabet or with frequency 0");
     }
     int64_t total = 0;
     for (const auto& st : h->streams) total += (int64_t)st.size();

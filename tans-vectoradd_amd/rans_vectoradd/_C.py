@@ -252,7 +252,10 @@ def fp8_gemm_fused_tans(m, decode_tbl: torch.Tensor, x: torch.Tensor,
     _require(m.states.numel() == K, "states do not match the matrix shape")
     _require(m.offsets.numel() == _groups(K) + 1, "offsets do not match the matrix shape")
     _require(m.sm.numel() == _sm_bytes(K, Nc), "sign/mantissa tiles do not match the matrix shape")
-    log2L = log2_states(decode_tbl.numel() // 2)
+    n_states = {"pair": 1 << TANS_PAIR_LOG2L, "nibble": 1 << TANS_NIBBLE_LOG2L}.get(m.alphabet)
+    _require(n_states is not None and decode_tbl.numel() == 2 * n_states,
+             f"decode_tbl must hold 2 words per state of the matrix's {m.alphabet} alphabet")
+    log2L = log2_states(n_states)
     dev = m.comp.device
     for t in (m.offsets, m.states, m.sm, decode_tbl, x2):
         _require(t.device == dev, "all tensors must be on one device")

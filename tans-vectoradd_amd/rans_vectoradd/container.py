@@ -38,9 +38,14 @@ def save(path: str, entries: dict, metadata: dict | None = None) -> None:
         if k.startswith("tans"):
             raise ValueError("metadata keys starting with 'tans' are reserved")
         meta[str(k)] = str(v)
+    encoded = {n for n, e in entries.items() if isinstance(e, (TansTensor, TansMatrix))}
     for name, e in entries.items():
-        if "." in name and isinstance(e, (TansTensor, TansMatrix)):
+        if "." in name and name in encoded:
             raise ValueError(f"encoded entry names may not contain '.': {name}")
+        stem, _, part = name.rpartition(".")
+        if name not in encoded and stem in encoded and part in _PARTS:
+            raise ValueError(f"plain tensor {name!r} would overwrite part {part!r} of the "
+                             f"encoded entry {stem!r}")
         if isinstance(e, TansTensor):
             desc = {"kind": "lanes", "K": e.K, "N": e.N, "alphabet": e.alphabet}
         elif isinstance(e, TansMatrix):

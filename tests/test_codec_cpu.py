@@ -161,7 +161,18 @@ def test_encoder_rejects_zero_frequency_symbol(T):
     freqs = torch.zeros(16, dtype=torch.int32)
     freqs[0] = 2048
     spread = torch.from_numpy(T.build_spread(freqs.numpy()))
-    with pytest.raises(RuntimeError, match="frequency is 0"):
+    with pytest.raises(RuntimeError, match="frequency 0"):
+        _C.tans_encode_interleaved(syms, freqs, spread)
+
+
+def test_encoder_rejects_symbol_outside_the_alphabet(T):
+    """Pair symbols coded with a 16-symbol table: the encoder reports
+    TANS_ESYMBOL instead of reading past its per-symbol tables."""
+    from rans_vectoradd import _C
+    syms = torch.full((64, 8), 200, dtype=torch.uint8)
+    freqs = torch.from_numpy(T.symbol_freqs(np.ones(16), "nibble"))
+    spread = torch.from_numpy(T.build_spread(freqs.numpy()))
+    with pytest.raises(RuntimeError, match="outside the alphabet"):
         _C.tans_encode_interleaved(syms, freqs, spread)
 
 

@@ -51,6 +51,21 @@ def test_container_roundtrip(tmp_path):
     assert np.array_equal(_decode_matrix(got["w"]), w.reshape(100, 70).numpy())
 
 
+def test_container_rejects_plain_names_that_shadow_encoded_parts(tmp_path):
+    """A plain tensor named '<entry>.<part>' would overwrite that part of an
+    encoded entry on save; save refuses it.  Other dotted names are fine."""
+    from rans_vectoradd import container, data as D, tans_codec as T
+    q, _ = D.gaussian_fp8_bytes(64 * 32, seed=2)
+    lanes = T.TansTensor.from_tuple(T.encode(q.reshape(64, 32), D.exp_histogram(q)), 64, 32, "pair")
+    path = os.path.join(tmp_path, "c.safetensors")
+    with pytest.raises(ValueError, match="overwrite"):
+        container.save(path, {"w": lanes, "w.comp": torch.zeros(5, dtype=torch.int32)})
+    container.save(path, {"w": lanes, "w.bias": torch.ones(3), "v.comp": torch.ones(2)})
+    got = container.load(path)
+    assert torch.equal(got["w"].comp, lanes.comp)
+    assert torch.equal(got["w.bias"], torch.ones(3)) and torch.equal(got["v.comp"], torch.ones(2))
+
+
 def test_container_rejects_other_files(tmp_path):
     from safetensors.torch import save_file
     from rans_vectoradd import container

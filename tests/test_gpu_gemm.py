@@ -128,5 +128,8 @@ def test_gemm_argument_errors(R):
         R.fp8_gemm_fused_tans(md, tbl, _x(1, 31, 0).cuda(), scale)       # wrong width
     with pytest.raises(RuntimeError):
         R.fp8_gemm_fused_tans(md, tbl, _x(1, 32, 0).float().cuda(), scale)   # not bf16
+    with pytest.raises(RuntimeError, match="alphabet"):
+        nib = T.encode_matrix(w, D.exp_histogram(w), alphabet="nibble").decode_table().cuda()
+        R.fp8_gemm_fused_tans(md, nib, _x(1, 32, 0).cuda(), scale)       # table of the other alphabet
     with pytest.raises(RuntimeError):
         R.fp8_gemm_raw(torch.zeros(4, 24, dtype=torch.uint8).cuda(), _x(1, 24, 0).cuda())
