@@ -117,6 +117,55 @@ def test_gemm_config3_shape_fused_vs_raw(R, B):
         assert bool((d <= 2.0 ** -7 * raw.float().abs() + 1e-6).all())
 
 
+@pytest.mark.parametrize("B", [2, 4, 8])
+@pytest.mark.parametrize("table", ["matched", "laplace"])
+def test_gemm_config4_down_shape(R, B, table):
+    """Config 4's W_down shape (5120 x 17408: 85 segments of 206 columns,
+    the last one ragged) at the batch sizes the bench times, with the
+    matrix's own table and with a mismatched (Laplace) one."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: gemm 5120x17408 B={B} {table} table")
+    w, scale = _weights(5120, 17408, seed=21)
+    x = _x(B, 17408, seed=22 + B)
+    if table == "matched":
+        hist = D.exp_histogram(w)
+    else:
+        hist = D.exp_histogram(D.laplace_fp8_bytes(1 << 20, seed=23)[0])
+    m = T.encode_matrix(w, hist)
+    assert m.segments == 85 and m.cols % m.seg_cols != 0
+    _check(_fused(R, m, x, scale), _reference(w, x, scale))
+
+
+@pytest.mark.parametrize("B", [2, 4])
+def test_gemm_config4_up_shape_batches(R, B):
+    """W_up (17408 x 5120, 28 segments) at the batch sizes between 1 and 8."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: gemm 17408x5120 B={B}")
+    w, scale = _weights(17408, 5120, seed=31)
+    x = _x(B, 5120, seed=32 + B)
+    m = T.encode_matrix(w, D.exp_histogram(w))
+    _check(_fused(R, m, x, scale), _reference(w, x, scale))
+
+
+def test_gemm_config4_layer_pair_chained(R):
+    """One config-4 layer as the bench runs it: y1 = W_up x (bf16), then
+    y2 = W_down y1, against the float64 chain (the intermediate rounded to
+    bf16 as the kernel's output is)."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say("case: gemm layer pair up -> down, B=4")
+    wu, su = _weights(17408, 5120, seed=41)
+    wd, sd = _weights(5120, 17408, seed=42, dist="laplace")
+    x = _x(4, 5120, seed=43)
+    mu = T.encode_matrix(wu, D.exp_histogram(wu))
+    md = T.encode_matrix(wd, D.exp_histogram(wd))
+    y1 = _fused(R, mu, x, su)
+    y2 = R.fp8_gemm_fused_tans(md.to("cuda"), md.decode_table().cuda(), y1, sd)
+    ref1 = _reference(wu, x, su)
+    _check(y1, ref1)
+    ref2 = _reference(wd, ref1.to(torch.bfloat16), sd)
+    _check(y2, ref2)
+
+
 def test_gemm_argument_errors(R):
     from rans_vectoradd import data as D, tans_codec as T
     w, scale = _weights(64, 32, seed=1)

@@ -230,6 +230,75 @@ def test_vecadd_gaussian_2p24(R, lut, alphabet):
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("N", [64, 256])
+def test_vecadd_gaussian_short_streams(R, lut, alphabet, N):
+    """Config-1 sweep points below the headline: 64 and 256 elements per
+    lane (4Ki- and 16Ki-element streams of 64 lanes), N(0, 0.02) data at
+    2^24 elements per vector, against the oracle's add table."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: fused vecadd gaussian 2^24, {N} per lane, {alphabet}")
+    n = 1 << 24
+    K = n // N
+    qa, _ = D.gaussian_fp8_bytes(n, seed=11)
+    qb, _ = D.gaussian_fp8_bytes(n, seed=12)
+    hist = D.exp_histogram(torch.cat([qa, qb]))
+    ea = T.encode(qa.reshape(K, N), hist, tile=8, alphabet=alphabet)
+    eb = T.encode(qb.reshape(K, N), hist, tile=8, alphabet=alphabet)
+    tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy())
+    order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
+    args = [x.cuda() for x in (*[ea[i] for i in order], *[eb[i] for i in order], tbl)]
+    fused = T.untile(R.fp8_vecadd_fused_tans(*args, N).cpu(), K, N).numpy()
+    ref = O.vecadd(lut, qa.numpy(), qb.numpy()).reshape(K, N)
+    assert np.array_equal(fused, ref)
+
+
+def _few_exponent_bytes(K, N, exps, seed):
+    """FP8 bytes whose exponent field takes only the values in `exps`
+    (random sign and mantissa, never a NaN)."""
+    g = torch.Generator().manual_seed(seed)
+    e = torch.tensor(exps, dtype=torch.int64)[torch.randint(0, len(exps), (K, N), generator=g)]
+    sm = torch.randint(0, 16, (K, N), generator=g)
+    m = sm & 7
+    m = torch.where(e == 15, torch.clamp(m, max=6), m)
+    return (((sm >> 3) << 7) | (e << 3) | m).to(torch.uint8)
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("exps_a,exps_b", [((7,), (7,)), ((15,), (15,)), ((0,), (9,)),
+                                           ((7, 8), (7, 8)), ((3,), (3, 12))])
+def test_few_exponents_zero_bit_steps(R, lut, alphabet, exps_a, exps_b):
+    """Tensors with one or two exponent values.  A one-exponent table gives
+    the single symbol the whole state space (f = L), so every step reads 0
+    bits and each lane's stream is one zero word (the reference guards
+    nb = 0 at csrc/vecadd.cu:128).  Decode returns the input, the fused add
+    equals the oracle's table, and the GPU encoder writes the CPU encoder's
+    bytes."""
+    from rans_vectoradd import tans_codec as T
+    _say(f"case: exponents {exps_a} + {exps_b} ({alphabet})")
+    K, N = 200, 48
+    fa = _few_exponent_bytes(K, N, exps_a, seed=1)
+    fb = _few_exponent_bytes(K, N, exps_b, seed=2)
+    hist = np.bincount(((torch.cat([fa, fb]).numpy() >> 3) & 15).ravel(), minlength=16)
+    ea = T.encode(fa, hist, tile=8, alphabet=alphabet)
+    eb = T.encode(fb, hist, tile=8, alphabet=alphabet)
+    if len(set(exps_a) | set(exps_b)) == 1:
+        tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy()).view(-1, 2)
+        assert ((tbl[:, 0] & 0x1F) == 0).all()          # every entry reads 0 bits
+    for f, e in ((fa, ea), (fb, eb)):
+        comp, st, off, part, sm, fr, sp = [x.cuda() for x in e]
+        dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
+        assert torch.equal(dec.cpu().t().contiguous(), f)
+        g = T.encode_gpu(f.cuda(), hist, tile=8, alphabet=alphabet)
+        for i in (0, 1, 2, 4, 5, 6):
+            assert torch.equal(g[i].cpu(), e[i]), f"GPU encoder output {i} differs"
+    tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy())
+    order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
+    args = [x.cuda() for x in (*[ea[i] for i in order], *[eb[i] for i in order], tbl)]
+    fused = T.untile(R.fp8_vecadd_fused_tans(*args, N).cpu(), K, N).numpy()
+    assert np.array_equal(fused, O.vecadd(lut, fa.numpy(), fb.numpy()).reshape(K, N))
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
 def test_streams_consumed_near_the_feed_limit(R, lut, alphabet):
     """Uniformly random bytes coded with a table built for a steep exponent
     histogram (p_e proportional to 2^-e): most symbols cost 8-12 bits, so
