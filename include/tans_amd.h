@@ -190,6 +190,22 @@ int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* off
                         const void* x, int64_t B, float scale, void* workspace,
                         int64_t workspace_bytes, void* y, void* stream);
 
+/* tans_fp8_gemm_fused without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc).  The partial sums go to a 16 MiB
+ * device array inside the library (one per GPU, held until the process
+ * ends), so S * B * Rp * 4 must not exceed 16 MiB (config 4's 17408 x 5120
+ * and 5120 x 17408 layers fit at B = 8); larger products return
+ * TANS_EINVAL.  Every call on one GPU uses that GPU's array: calls that
+ * overlap in time on one GPU (different streams, host threads) race on it
+ * and must be ordered by the caller.  Otherwise the same arguments, checks
+ * and results as tans_fp8_gemm_fused.                                     */
+int tans_fp8_gemm_fused_noalloc(const void* comp, int64_t comp_bytes, const int64_t* offsets,
+                                const uint16_t* states, const void* sm, const uint32_t* table,
+                                int32_t log2L, int64_t R, int64_t C, int64_t S, int64_t Nc,
+                                const void* x, int64_t B, float scale, void* y, void* stream);
+
 /* The same product from uncompressed FP8 W [R, C] (row-major), C % 16 == 0:
  * the baseline the fused kernel is measured against.                    */
 int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_t B,

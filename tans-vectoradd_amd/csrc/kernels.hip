@@ -46,6 +46,7 @@
 #include <algorithm>
 #include <atomic>
 #include <climits>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -1315,6 +1316,40 @@ int sps_for(int32_t log2L) {
 template <int SPS>
 constexpr int kFusedGroups = 1;   // groups per wave in the fused kernel
 
+int gemm_fused_launch(const void* comp, int64_t comp_bytes, const int64_t* offsets,
+                      const uint16_t* states, const void* sm, const uint32_t* table,
+                      int32_t log2L, int64_t R, int64_t C, int64_t S, int64_t Nc, const void* x,
+                      int64_t B, float scale, void* workspace, int64_t workspace_bytes, void* y,
+                      void* stream);
+
+// Device scratch of tans_fp8_gemm_fused_noalloc: the per-segment partial
+// sums live in this file-scope array, so that entry point allocates
+// nothing.  Each GPU holds its own copy for the life of the process.  In
+// host code `scratch` is only a handle: its device address on the current
+// GPU comes from hipGetSymbolAddress, looked up once per device and kept.
+constexpr int64_t kGemmScratchBytes = int64_t(16) << 20;
+static __device__ __align__(256) float scratch[kGemmScratchBytes / 4];
+
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices];
+
+int scratch_address(void** out) {
+    int dev = -1;
+    int rc = hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (rc != TANS_OK) return rc;
+    if (dev < 0 || dev >= kMaxDevices) return fail(TANS_EINVAL, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                       "hipGetSymbolAddress(scratch)");
+        if (rc != TANS_OK) return rc;
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return TANS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1436,6 +1471,37 @@ int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* off
                         int32_t log2L, int64_t R, int64_t C, int64_t S, int64_t Nc, const void* x,
                         int64_t B, float scale, void* workspace, int64_t workspace_bytes, void* y,
                         void* stream) {
+    return gemm_fused_launch(comp, comp_bytes, offsets, states, sm, table, log2L, R, C, S, Nc, x,
+                             B, scale, workspace, workspace_bytes, y, stream);
+}
+
+int tans_fp8_gemm_fused_noalloc(const void* comp, int64_t comp_bytes, const int64_t* offsets,
+                                const uint16_t* states, const void* sm, const uint32_t* table,
+                                int32_t log2L, int64_t R, int64_t C, int64_t S, int64_t Nc,
+                                const void* x, int64_t B, float scale, void* y, void* stream) {
+    // S * B * Rp floats of partial sums must fit the scratch array
+    // (compared by division, so no product can overflow)
+    const int64_t cap = kGemmScratchBytes / 4;
+    const int64_t Rp = R > 0 && R <= cap ? (R + kLanes - 1) / kLanes * kLanes : cap + 1;
+    if (R > 0 && S > 0 && B > 0 && (Rp > cap || S > cap / Rp || B > cap / (S * Rp)))
+        return fail(TANS_EINVAL, "gemm_fused_noalloc: S * B * Rp * 4 bytes of partial sums "
+                                 "exceed the 16 MiB device scratch buffer");
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc != TANS_OK) return rc;
+    return gemm_fused_launch(comp, comp_bytes, offsets, states, sm, table, log2L, R, C, S, Nc, x,
+                             B, scale, ws, kGemmScratchBytes, y, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int gemm_fused_launch(const void* comp, int64_t comp_bytes, const int64_t* offsets,
+                      const uint16_t* states, const void* sm, const uint32_t* table,
+                      int32_t log2L, int64_t R, int64_t C, int64_t S, int64_t Nc, const void* x,
+                      int64_t B, float scale, void* workspace, int64_t workspace_bytes, void* y,
+                      void* stream) {
     const int sps = sps_for(log2L);
     if (!sps) return fail(TANS_EINVAL, "gemm_fused: log2L must be 12 (pair) or 11 (nibble)");
     if (R <= 0 || C <= 0 || S <= 0 || Nc <= 0 || Nc % 2)
@@ -1481,6 +1547,10 @@ int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* off
                        R, scale, (uint16_t*)y);
     return hip_check(hipGetLastError(), "gemm_finalize_kernel launch");
 }
+
+}  // namespace
+
+extern "C" {
 
 int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_t B, float scale,
                       void* y, void* stream) {

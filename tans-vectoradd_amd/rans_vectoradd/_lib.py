@@ -25,6 +25,7 @@ EXPORTS = (
     "tans_fp8_vecadd_fused",
     "tans_decode",
     "tans_fp8_gemm_fused",
+    "tans_fp8_gemm_fused_noalloc",
     "tans_fp8_gemm_raw",
     "tans_build_encode_table",
     "tans_gpu_encode_workspace",
@@ -66,6 +67,8 @@ for _name, _args in {
     "tans_decode": [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I64, _P, _P],
     "tans_fp8_gemm_fused": [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _I64,
                             ctypes.c_float, _P, _I64, _P, _P],
+    "tans_fp8_gemm_fused_noalloc": [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P,
+                                    _I64, ctypes.c_float, _P, _P],
     "tans_fp8_gemm_raw": [_P, _I64, _I64, _P, _I64, ctypes.c_float, _P, _P],
     "tans_build_encode_table": [_P, _P, _I32, _I32, _P, _P],
     "tans_gpu_encode_workspace": [_I64, _I64, _I32, ctypes.POINTER(_I64)],
