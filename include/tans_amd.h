@@ -24,18 +24,22 @@
  *     read LSB first; every decode step reads nb bits as one value.  The
  *     words of the 64 lanes of group g form one stream at
  *     comp_words[offsets[g] ..], ordered by the refill schedule all decoders
- *     follow: each lane starts with an empty buffer; before every second
- *     step (steps 0, 2, 4, ...) each active lane holding fewer than 24 bits
- *     takes the next stream word (lanes in ascending order) and gains 32
- *     bits.  Streams start on 16-byte boundaries; 1 KiB of zero words
- *     follows the last one.  offsets is int64 [n_groups + 1], in words.
+ *     follow: every active lane starts with two words (the stream's first
+ *     words go to lanes 0, 1, ... in turn, then their second words); after
+ *     each step pair (steps 2p, 2p + 1) except the last, each active lane
+ *     holding at most 32 unread bits takes the next stream word (lanes in
+ *     ascending order) and gains 32 bits; after the second-to-last pair only
+ *     a lane holding fewer than 24 bits does.  Streams start on 16-byte
+ *     boundaries; 1 KiB of zero words follows the last one.  offsets is
+ *     int64 [n_groups + 1], in words.
  *   - states[k] is lane k's initial decoder state in [L, 2L).
  *   - Sign/mantissa nibbles: 16-element tiles, 8 bytes per (tile, lane) at
  *     sm[(t * K + k) * 8]; u32 word h covers elements 8h..8h+7 as
  *     (A & 0x87878787) | rotl(B & 0x87878787, 4), A/B being elements
  *     8h..8h+3 / 8h+4..8h+7 read as little-endian words.
  *   - Decode table: L entries of two u32 words:
- *       word0 = nb | (e0 << 11) | (e1 << 19)   (nibble alphabet: nb | e << 11)
+ *       word0 = nb | (e0 << 11) | (e1 << 19) | (nb << 27)
+ *               (nibble alphabet: nb | (e << 11) | (nb << 27))
  *       word1 = (base - L) * 8
  *     for the state x = L + slot, with x_prev = f_sym + rank,
  *     nb = doublings of x_prev until >= L, base = x_prev << nb.

@@ -373,9 +373,11 @@ int ora_ref_decode_add(const uint8_t* a_comp8, const int32_t* a_off, const uint1
  *   column j = k%64.  Each lane's decode-order bits are cut into u32 words
  *   (LSB = earliest bit); each decode step reads nb bits as one value.
  *   Group g's words form one stream at comp_words[offsets[g] ..], in the
- *   order of this refill schedule: every lane starts with 0 buffered bits;
- *   before steps 0, 2, 4, ... each active lane (ascending j) holding fewer
- *   than 24 unread bits takes the next stream word (+32 bits).
+ *   order of this refill schedule: first every active lane (ascending j)
+ *   takes one word, then every active lane takes a second; after each step
+ *   pair (steps 2p, 2p+1) except the last, each active lane (ascending j)
+ *   holding at most 32 unread bits takes the next stream word (+32 bits),
+ *   and after the second-to-last pair only a lane holding fewer than 24.
  *   states[k] is the initial decoder state in [L, 2L).
  *   Symbols: sps=2 -> pair symbol e0*16+e1 per step; sps=1 -> one exponent.
  *   Sign/mantissa: tiles of 16 elements, 8 bytes per (tile, lane) at
@@ -466,16 +468,15 @@ int ora_w64_decode(const uint8_t* comp8, const int64_t* offsets, const uint16_t*
             if (ln[j].x < L || ln[j].x >= 2 * L) bad = -10;
         }
         int64_t pos = offsets[g], end = offsets[g + 1];
-        for (int64_t i = 0; i < steps && !bad; i++) {
-            if (i % 2 == 0) {
+        if (steps > 0) {
+            for (int r = 0; r < 2 && !bad; r++)
                 for (int j = 0; j < lanes && !bad; j++) {
-                    uint64_t avail = (uint64_t)ln[j].n_words * 32 - ln[j].rd;
-                    if (avail < 24) {
-                        if (pos >= end) { bad = -12; break; }
-                        if (lane_take(&ln[j], comp[pos++])) bad = -15;
-                    }
+                    if (pos >= end) { bad = -12; break; }
+                    if (lane_take(&ln[j], comp[pos++])) bad = -15;
                 }
-            }
+        }
+        const int64_t pairs = (steps + 1) / 2;
+        for (int64_t i = 0; i < steps && !bad; i++) {
             for (int j = 0; j < lanes && !bad; j++) {
                 int64_t k = g * 64 + j;
                 uint32_t slot = ln[j].x - L;
@@ -487,6 +488,17 @@ int ora_w64_decode(const uint8_t* comp8, const int64_t* offsets, const uint16_t*
                 out[k * N + el] = compose_fp8((uint32_t)e0, sm_nibble_of(sm8, (int)(el % 16)));
                 if (sps == 2)
                     out[k * N + el + 1] = compose_fp8((uint32_t)e1, sm_nibble_of(sm8, (int)((el + 1) % 16)));
+            }
+            const int64_t p = i / 2;
+            if ((i % 2 == 1 || i == steps - 1) && p + 1 < pairs) {
+                const uint64_t below = (p + 2 == pairs) ? 24 : 33;
+                for (int j = 0; j < lanes && !bad; j++) {
+                    uint64_t avail = (uint64_t)ln[j].n_words * 32 - ln[j].rd;
+                    if (avail < below) {
+                        if (pos >= end) { bad = -12; break; }
+                        if (lane_take(&ln[j], comp[pos++])) bad = -15;
+                    }
+                }
             }
         }
         for (int j = 0; j < lanes && !bad; j++) {

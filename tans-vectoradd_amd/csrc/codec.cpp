@@ -38,11 +38,15 @@ inline uint32_t rotl32(uint32_t v, int r) { return (v << r) | (v >> (32 - r)); }
 
 inline int ilog2(uint32_t v) { return 31 - __builtin_clz(v); }
 
-// Refill schedule shared with the decoders: before every second step a lane
-// whose buffer holds fewer than kRefillBelow bits takes the next 32-bit word
-// of its group's stream (lanes in ascending order).  Two steps read at most
-// 2*12 bits, so the buffer never runs dry and never exceeds 64 bits.
-constexpr int kRefillBelow = 24;
+// Refill schedule shared with the decoders: every lane starts with two
+// 32-bit words of its group's stream (the first words of lanes 0, 1, ...,
+// then their second words).  After each step pair (steps 2p, 2p + 1) but the
+// last, a lane holding at most 32 unread bits takes the next word (lanes in
+// ascending order); after the second-to-last pair only a lane holding fewer
+// than 24 does.  Two steps read at most 2 * 12 bits, so the 64-bit buffer
+// never runs dry and never overflows.
+constexpr int kRefillAtMost = 32;
+constexpr int kRefillFinalBelow = 24;
 // Zero words appended after the last group, so 16-byte segment loads near
 // the end stay inside the buffer.
 constexpr int64_t kTailWords = 256;
@@ -180,7 +184,7 @@ int tans_build_decode_table(const int32_t* spread, const int32_t* freqs, int32_t
         const int nb = log2L - ilog2(xp);
         const uint32_t base = xp << nb;
         const uint32_t ex = (nsym == 256) ? (((s >> 4) << 11) | ((s & 0xF) << 19)) : (s << 11);
-        table[2 * slot] = (uint32_t)nb | ex;
+        table[2 * slot] = (uint32_t)nb | ex | ((uint32_t)nb << 27);
         table[2 * slot + 1] = (base - L) * 8u;
     }
     return TANS_OK;
@@ -225,7 +229,6 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
         return fail(TANS_ENOMEM, "encode: out of memory");
     }
     const int64_t max_words = (S * (int64_t)log2L + 31) / 32 + 1;
-    const int64_t n_checks = (S + 1) / 2;
     int bad_symbol = 0;
     #pragma omp parallel
     {
@@ -253,18 +256,25 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
             // Replay the decoders' refill schedule to order the words.
             std::vector<uint32_t>& out = h->streams[(size_t)g];
             out.clear();
-            out.reserve((size_t)(lanes * (max_words + 2)));
+            out.reserve((size_t)(lanes * (max_words + 3)));
+            auto take = [&](int j) {
+                const int64_t r = taken[j]++;
+                out.push_back(r < nw[j] ? words[(size_t)(j * max_words + r)] : 0u);
+                cnt[j] += 32;
+            };
             for (int j = 0; j < lanes; j++) { cnt[j] = 0; taken[j] = 0; }
-            for (int64_t q = 0; q < n_checks; q++) {
+            if (S > 0) {
+                for (int r = 0; r < 2; r++)
+                    for (int j = 0; j < lanes; j++) take(j);
+            }
+            const int64_t n_pairs = (S + 1) / 2;
+            for (int64_t q = 0; q + 1 < n_pairs; q++) {
+                const int32_t below = (q + 2 == n_pairs) ? kRefillFinalBelow : kRefillAtMost + 1;
                 for (int j = 0; j < lanes; j++) {
-                    if (cnt[j] < kRefillBelow) {
-                        const int64_t r = taken[j]++;
-                        out.push_back(r < nw[j] ? words[(size_t)(j * max_words + r)] : 0u);
-                        cnt[j] += 32;
-                    }
                     const uint32_t* ch = chunk.data() + j * S;
                     cnt[j] -= (int32_t)(ch[2 * q] >> 16);
                     if (2 * q + 1 < S) cnt[j] -= (int32_t)(ch[2 * q + 1] >> 16);
+                    if (cnt[j] < below) take(j);
                 }
             }
             while (out.size() % 4) out.push_back(0u);

@@ -33,7 +33,8 @@ namespace {
 
 constexpr int kLanes = 64;
 constexpr int kTile = 16;
-constexpr int kRefillBelow = 24;   // the decoders' refill threshold
+constexpr int kRefillAtMost = 32;      // the decoders' refill rule: take at <= 32 unread bits
+constexpr int kRefillFinalBelow = 24;  // after the second-to-last step pair: below 24
 constexpr int64_t kTailWords = 256;
 constexpr int kEncBlock = 256;
 
@@ -59,8 +60,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // Workspace layout: chunks u16 [S][K], words u32 [max_words][K],
-// nwords u32 [K], glen u32 [G], takes u32 [ceil(checks / 32)][K] (bit q % 32
-// of word q / 32: the lane takes a word at refill check q).
+// nwords u32 [K], glen u32 [G], takes u32 [ceil(pairs / 32)][K] (bit q % 32
+// of word q / 32: the lane takes a word after step pair q).
 struct WsLayout {
     int64_t chunks, words, nwords, glen, takes, total;
 };
@@ -225,10 +226,12 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     if (bad >> 31) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
 }
 
-// The refill schedule: before step 2q each active lane holding fewer than
-// 24 bits takes the next word (+32 bits), then steps 2q and 2q + 1 consume
-// their nb bits.  This pass replays it while it packs each lane's chunks
-// into words, and records per check whether the lane takes a word, so
+// The refill schedule: every active lane starts with two words (64 bits);
+// steps 2q and 2q + 1 consume their nb bits, and after that step pair, if
+// it is not the last, a lane holding at most 32 bits takes the next word
+// (+32 bits); after the second-to-last pair only a lane holding fewer than
+// 24 does.  This pass replays it while it packs each lane's chunks into
+// words, and records per pair whether the lane takes a word, so
 // enc_interleave_kernel needs only those bits.  Chunks are read 16 steps at
 // a time (a step past S reads as an empty chunk).
 constexpr int kPackChecks = 8;
@@ -248,9 +251,13 @@ __global__ __launch_bounds__(kEncBlock) void enc_pack_kernel(
     int n = 0;
     uint32_t nw = 0, taken = 0, tw = 0;
     int cnt = 0;
-    const int64_t n_checks = (S + 1) / 2;
-    static_assert(32 % kPackChecks == 0, "a batch of checks never straddles a takes word");
-    for (int64_t q0 = 0; q0 < n_checks; q0 += kPackChecks) {
+    if (S > 0) {
+        taken = 2;
+        cnt = 64;
+    }
+    const int64_t n_pairs = (S + 1) / 2;
+    static_assert(32 % kPackChecks == 0, "a batch of pairs never straddles a takes word");
+    for (int64_t q0 = 0; q0 < n_pairs; q0 += kPackChecks) {
         uint32_t c[2 * kPackChecks];
         #pragma unroll
         for (int u = 0; u < 2 * kPackChecks; u++) {
@@ -259,12 +266,8 @@ __global__ __launch_bounds__(kEncBlock) void enc_pack_kernel(
         }
         #pragma unroll
         for (int u = 0; u < kPackChecks; u++) {
-            if (q0 + u >= n_checks) break;   // wave-uniform
-            if (cnt < kRefillBelow) {
-                taken++;
-                cnt += 32;
-                tw |= 1u << ((q0 + u) % 32);
-            }
+            const int64_t q = q0 + u;
+            if (q >= n_pairs) break;   // wave-uniform
             #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const uint32_t ch = c[2 * u + h];
@@ -279,9 +282,17 @@ __global__ __launch_bounds__(kEncBlock) void enc_pack_kernel(
                     n -= 32;
                 }
             }
+            if (q + 1 < n_pairs) {   // wave-uniform: no check after the last pair
+                const int below = q + 2 == n_pairs ? kRefillFinalBelow : kRefillAtMost + 1;
+                if (cnt < below) {
+                    taken++;
+                    cnt += 32;
+                    tw |= 1u << (q % 32);
+                }
+            }
         }
         const int64_t qe = q0 + kPackChecks;
-        if (qe % 32 == 0 || qe >= n_checks) {   // wave-uniform
+        if (qe % 32 == 0 || qe >= n_pairs) {   // wave-uniform
             if (active) takes[(q0 / 32) * K + k] = tw;
             tw = 0;
         }
@@ -331,10 +342,11 @@ __global__ __launch_bounds__(kEncBlock) void zero_words_kernel(uint32_t* __restr
     if (i < n) p[i] = 0u;
 }
 
-// Replays the schedule from the take bits of enc_pack_kernel: at each check
-// the lanes taking a word write it at offset + handed + rank (ballot +
-// mbcnt, the order the decoders read), 32 checks per take word with the
-// word loads of 8 checks issued together.
+// Replays the schedule from the take bits of enc_pack_kernel: first the two
+// initial words of every active lane (the first words in lane order, then
+// the second), then after each step pair the lanes taking a word write it
+// at offset + handed + rank (ballot + mbcnt, the order the decoders read),
+// 32 pairs per take word with the word loads of 8 pairs issued together.
 __global__ __launch_bounds__(kEncBlock) void enc_interleave_kernel(
     const uint32_t* __restrict__ takes, int64_t K, int64_t S, int64_t max_words,
     const uint32_t* __restrict__ words, const uint32_t* __restrict__ nwords,
@@ -350,7 +362,18 @@ __global__ __launch_bounds__(kEncBlock) void enc_interleave_kernel(
     const int64_t end = offsets[g + 1];
     int64_t handed = 0;
     uint32_t taken = 0;
-    const int64_t n_checks = (S + 1) / 2;
+    if (S > 0) {
+        const int64_t lanes = K - g * kLanes < kLanes ? K - g * kLanes : kLanes;
+        #pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int64_t pos = base + r * lanes + lane;
+            if (active && pos < end)
+                comp[pos] = (uint32_t)r < nw && r < max_words ? words[(int64_t)r * K + k] : 0u;
+        }
+        handed = 2 * lanes;
+        taken = 2;
+    }
+    const int64_t n_checks = (S + 1) / 2 - 1;   // a check after every step pair but the last
     constexpr int kBatch = 8;
     for (int64_t q0 = 0; q0 < n_checks; q0 += 32) {
         const uint32_t tw = active ? takes[(q0 / 32) * K + k] : 0u;

@@ -19,23 +19,30 @@
 // Decoder design.  One wave64 decodes one 64-lane group; each lane owns one
 // tANS state.  The decode table lives in LDS as 8-byte entries addressed by
 // a byte offset kept in the state register.  A lane's unread bits sit in a
-// 64-bit window (hi:lo) read from bit `pos`; one step is a ds_read_b64 of
-// the entry, a 64-bit shift of the window, a bit-field extract of nb bits,
-// one shift-add for the next entry's offset and pos += nb.
+// 64-bit window (hi:lo) read from bit pos of lo (0 <= pos < 32).  Steps go
+// in pairs: one funnel shift takes the 32 bits from pos (two steps read at
+// most 24), each step is a ds_read_b64 of the entry, a bit-field extract of
+// nb bits and one shift-add for the next entry's offset, and pos advances
+// by nb1 + nb2 in a register that holds pos both in bits 4:0 and in bits
+// 31:27 (the table holds nb in both places), so the add's carry out is set
+// exactly when lo is used up.
 //
-// Before every second step, each lane holding fewer than 24 unread bits
-// takes the next word of the group's stream: the ballot of those lanes, an
-// mbcnt for each lane's rank and one ds_read_b32 from the wave's LDS ring.
-// The ring holds kSlots segments of 256 words (one 16-byte load per lane)
-// plus a 64-word mirror of its first words, so a wave's 64 consecutive reads
-// never wrap.  A stage issues at most one segment load per stream, through
-// a buffer resource whose bound is the room left in the stream, once the
-// segment's ring slot is free.  The loaded segment stays in registers and is
-// written into the ring no earlier than the next stage and no later than
-// the stage in which a lane could first take one of its words.  A stage is
-// four refill checks, so at most 256 words are handed out per stage, and
-// kSlots = kDelay + 2 slots guarantee that a fetched segment starts more
-// than a stage's worth of words ahead of the lanes.
+// That carry drives the refill: after each step pair but the last, the
+// lanes whose lo is used up move hi into lo and take the next word of the
+// group's stream (the carry mask, an mbcnt for each lane's rank and one
+// ds_read_b32 from the wave's LDS ring); after the second-to-last pair a
+// lane takes a word only below 24 unread bits.  Each lane starts with two
+// words.  The ring holds kSlots segments of 256 words (one 16-byte load per
+// lane) plus a 64-word mirror of its first words, so a wave's 64
+// consecutive reads never wrap.  A stage issues at most one segment load
+// per stream, through a buffer resource whose bound is the room left in
+// the stream, once the segment's ring slot is free.  The loaded segment
+// stays in registers and is written into the ring no earlier than the next
+// stage and no later than the stage in which a lane could first take one of
+// its words.  A stage is four refill checks, so at most 256 words are
+// handed out per stage, and kSlots = kDelay + 2 slots guarantee that a
+// fetched segment starts more than a stage's worth of words ahead of the
+// lanes.
 //
 // FP8 bytes are rebuilt four at a time: the table carries each exponent
 // pre-shifted to bits 6:3 of a byte, a v_perm gathers four of them and one
@@ -222,7 +229,7 @@ __global__ __launch_bounds__(kTableWaves * 64) void table_kernel(
         const int nb = top < log2L ? log2L - top : 0;
         const uint32_t base = xp << nb;
         const uint32_t ex = (nsym == 256) ? (((sv >> 4) << 11) | ((sv & 0xFu) << 19)) : (sv << 11);
-        table[seg * 64 + lane] = v2u{(uint32_t)nb | ex, (base - L) * 8u};
+        table[seg * 64 + lane] = v2u{(uint32_t)nb | ex | ((uint32_t)nb << 27), (base - L) * 8u};
     }
 }
 
@@ -246,7 +253,6 @@ __device__ __forceinline__ Rsrc rsrc(const void* base, uint32_t bytes) {
 // ---------------------------------------------------------------------
 // Decoder building blocks.
 // ---------------------------------------------------------------------
-constexpr int kRefillBelow = 24;           // a lane with fewer unread bits takes a word
 typedef v4u Seg;                           // one segment: 16 bytes per lane
 constexpr int kSegWords = 4 * kLanes;
 constexpr int kChecksPerStage = 4;         // a stage is 4 refill checks (8 steps)
@@ -282,8 +288,8 @@ struct Feed {
 
 // Per-lane decoder state.
 struct Lane {
-    uint32_t lo, hi;   // 64-bit window of stream bits, bit `pos` is the next unread one
-    int32_t pos;       // active lanes: [0, 64]; idle lanes: far below 0, never refill
+    uint32_t lo, hi;   // 64-bit window of stream bits; the next unread bit is bit pos of lo
+    uint32_t q;        // pos (0..31) in bits 4:0 and again in bits 31:27; bits 26:5 scratch
     uint32_t x8;       // (state - L) * 8: byte offset of the state's table entry
 };
 
@@ -372,43 +378,101 @@ __device__ __forceinline__ void feed_stage(Feed& f, Seg& pend, int lane) {
     }
 }
 
-// Refill check: lanes with fewer than 24 unread bits take the next words of
-// the stream, in lane order.  Every lane reads the ring (in bounds: the
-// mirror covers the 64 words past the ring end); only those that need a
-// word keep it, so there is no divergent branch.
-__device__ __forceinline__ void refill(Lane& l, Feed& f) {
-    const bool need = l.pos > 64 - kRefillBelow;
-    const uint64_t m = __ballot(need);
-    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+// A lane mask of the wave (one bit per lane, held in an SGPR pair).
+typedef uint64_t Mask;
+
+// x += y with the carry out of every lane as a lane mask (v_add_co_u32 with
+// an SGPR carry).  Written out because the compiler turns the carry of an
+// overflow add into a 0/1 VGPR and compares it again before a ballot.
+__device__ __forceinline__ Mask add_carry(uint32_t& x, uint32_t y) {
+    Mask c;
+    asm("v_add_co_u32 %0, %1, %2, %3" : "=v"(x), "=s"(c) : "v"(x), "v"(y));
+    return c;
+}
+
+// m's lanes take if_set, the others if_clear (v_cndmask_b32 on the mask).
+__device__ __forceinline__ uint32_t select(Mask m, uint32_t if_set, uint32_t if_clear) {
+    return __builtin_amdgcn_inverse_ballot_w64(m) ? if_set : if_clear;
+}
+
+// Two tANS steps.  One funnel shift gives the 32 bits from pos (two steps
+// read at most 24); each step is a ds_read_b64 of the entry, a bit-field
+// extract of nb bits (the second at offset nb1) and a shift-add for the next
+// entry's offset.  q advances by nb1 + nb2 in both of its copies with one
+// add (word0 holds nb in bits 4:0 and 30:27): the add's carry out is set
+// exactly when the low window word is used up.  Returns the carry mask;
+// w1/w2 get the two entries' word0.
+__device__ __forceinline__ Mask dec_pair(Lane& l, const v2u* __restrict__ tbl, uint32_t& w1,
+                                         uint32_t& w2) {
+    const uint32_t t = __builtin_amdgcn_alignbit(l.hi, l.lo, l.q);   // shift = q[4:0]
+    const v2u e1 = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
+    const uint32_t b1 = __builtin_amdgcn_ubfe(t, 0u, e1.x);           // width = nb1
+    l.x8 = (b1 << 3) + e1.y;
+    const v2u e2 = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
+    const uint32_t b2 = __builtin_amdgcn_ubfe(t, e1.x, e2.x);          // offset nb1, width nb2
+    l.x8 = (b2 << 3) + e2.y;
+    w1 = e1.x;
+    w2 = e2.x;
+    return add_carry(l.q, e1.x + e2.x);
+}
+
+// Lanes in `need` take the next words of the stream in lane order (mbcnt
+// rank, one ds_read_b32 from the ring); lanes in `shift` (a superset) move
+// hi into lo.  Every lane reads the ring (in bounds: the mirror covers the
+// 64 words past the ring end), so there is no divergent branch.
+__device__ __forceinline__ void refill(Lane& l, Feed& f, Mask shift, Mask need) {
+    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(need >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)need, 0u));
     const uint32_t w = *reinterpret_cast<const uint32_t*>(
         reinterpret_cast<const char*>(f.ring) + f.ring_b + rank * 4u);
-    l.lo = need ? l.hi : l.lo;
-    l.hi = need ? w : l.hi;
-    l.pos = need ? l.pos - 32 : l.pos;
-    const uint32_t c = (uint32_t)__popcll(m);
+    l.lo = select(shift, l.hi, l.lo);
+    l.hi = select(need, w, l.hi);
+    const uint32_t c = (uint32_t)__popcll(need);
     f.handed += c;
     const uint32_t nb = f.ring_b + c * 4u;
     const uint32_t wrapped = nb - (uint32_t)(kRingWords * 4);
     f.ring_b = nb < wrapped ? nb : wrapped;   // (nb mod ring size), as an unsigned min
 }
 
-// One tANS step.  Returns the entry's word0: nb in bits 4:0, exponents in
-// bits 14:11 (and 22:19 for a pair symbol).
-__device__ __forceinline__ uint32_t dec_step(Lane& l, const v2u* __restrict__ tbl) {
-    const v2u e = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
-    const uint64_t win = ((uint64_t)l.hi << 32) | l.lo;
-    const uint32_t t = (uint32_t)(win >> (l.pos & 63));
-    const uint32_t bits = __builtin_amdgcn_ubfe(t, 0u, e.x);   // width = e.x[4:0]
-    l.x8 = (bits << 3) + e.y;
-    l.pos += (int32_t)(e.x & 0xFFu);
-    return e.x;
+// The refill check after a step pair (`carry` from dec_pair, `active` the
+// lanes in range).  A lane whose low window word is used up (at most 32
+// unread bits) shifts and takes the next word.  After the second-to-last
+// step pair of the stream (final_check) it still shifts but takes a word
+// only below 24 unread bits (pos > 8 after the shift), since the last pair
+// reads at most 24.  There is no check after the last pair.
+__device__ __forceinline__ void check(Lane& l, Feed& f, Mask carry, Mask active,
+                                      bool final_check) {
+    const Mask shift = carry & active;
+    if (final_check) {
+        refill(l, f, shift, shift & __ballot((l.q & 31u) > 8u));
+    } else {
+        refill(l, f, shift, shift);
+    }
 }
 
-__device__ __forceinline__ void lane_init(Lane& l, bool active, uint16_t state, uint32_t L) {
-    l.lo = l.hi = 0;
-    l.pos = active ? 64 : -(1 << 30);
+// check() in the last tile, with its kind chosen at run time (wave-uniform
+// flags selecting lane masks): none after the stream's last step pair, the
+// final check after the second-to-last one.
+__device__ __forceinline__ void check_last(Lane& l, Feed& f, Mask carry, Mask active,
+                                           bool final_check, bool none) {
+    const Mask below24 = __ballot((l.q & 31u) > 8u);
+    const Mask shift = none ? Mask(0) : carry & active;
+    refill(l, f, shift, final_check ? shift & below24 : shift);
+}
+
+// Start a chain (after feed_commit): every active lane takes two words, the
+// first `lanes` stream words being the lanes' first words and the next
+// `lanes` their second; pos = 0.
+__device__ __forceinline__ void lane_init(Lane& l, Feed& f, int lane, int lanes, uint16_t state,
+                                          uint32_t L) {
+    const bool active = lane < lanes;
+    const uint32_t* r = f.ring;
+    l.lo = active ? r[lane] : 0u;
+    l.hi = active ? r[lanes + lane] : 0u;
+    l.q = 0;
     l.x8 = ((uint32_t)(state - L) & (L - 1)) * 8u;
+    f.handed = 2u * (uint32_t)lanes;
+    f.ring_b = 8u * (uint32_t)lanes;
 }
 
 // Exponent fields of four consecutive elements, from two pair steps or four
@@ -459,7 +523,8 @@ __device__ __forceinline__ void table_store(v2u* lds, const TableRegs<L>& r) {
         v2u e = r.e[k];
         const uint32_t nb = e.x & 0xFFu;
         const uint32_t base = e.y >> 3;
-        if (nb > log2L || (e.y & 7u) || base + (1u << nb) > L) e = v2u{e.x & ~0xFFu, 0u};
+        if (nb > log2L || (e.x >> 27) != nb || (e.y & 7u) || base + (1u << nb) > L)
+            e = v2u{e.x & 0x07FFFF00u, 0u};
         lds[threadIdx.x + k * kDecBlock] = e;
     }
 }
@@ -511,10 +576,17 @@ struct Chains {
 };
 
 // Decode the 16 elements of one tile of every chain into exponent words
-// ex[c][4] (4 elements each).
-template <int SPS, int C>
+// ex[c][4] (4 elements each).  q's scratch bits are cleared first (a step
+// pair adds less than 2^24 there).  LAST: the tile holds each stream's
+// final step pairs, last_pairs of them (the rest of the tile decodes past
+// the end: no checks there, so it reads only the lane's own window and the
+// table, and its bytes are discarded).
+template <int SPS, int C, bool LAST>
 __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ tbl, int lane,
-                                         uint32_t (&ex)[C][4]) {
+                                         uint32_t (&ex)[C][4], const Mask (&act)[C],
+                                         int last_pairs = 4 * Alpha<SPS>::kStagesPerTile) {
+    #pragma unroll
+    for (int c = 0; c < C; c++) ch.l[c].q &= 0xF800001Fu;
     static_for<0, Alpha<SPS>::kStagesPerTile>([&](auto H) {
         constexpr int h = decltype(H)::value;
         #pragma unroll
@@ -522,12 +594,23 @@ __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ 
         uint32_t e[C][8];
         #pragma unroll
         for (int q = 0; q < kChecksPerStage; q++) {
+            Mask carry[C];
             #pragma unroll
-            for (int c = 0; c < C; c++) refill(ch.l[c], ch.f[c]);
-            #pragma unroll
-            for (int c = 0; c < C; c++) e[c][2 * q] = dec_step(ch.l[c], tbl);
-            #pragma unroll
-            for (int c = 0; c < C; c++) e[c][2 * q + 1] = dec_step(ch.l[c], tbl);
+            for (int c = 0; c < C; c++)
+                carry[c] = dec_pair(ch.l[c], tbl, e[c][2 * q], e[c][2 * q + 1]);
+            if (LAST) {
+                // the step pair's index in the tile: pairs from last_pairs - 1
+                // on end the streams (no check) and the one before them gets
+                // the final check; selected on the masks, without branches
+                const int idx = h * kChecksPerStage + q;
+                #pragma unroll
+                for (int c = 0; c < C; c++)
+                    check_last(ch.l[c], ch.f[c], carry[c], act[c], idx == last_pairs - 2,
+                               idx >= last_pairs - 1);
+            } else {
+                #pragma unroll
+                for (int c = 0; c < C; c++) check(ch.l[c], ch.f[c], carry[c], act[c], false);
+            }
         }
         #pragma unroll
         for (int c = 0; c < C; c++) {
@@ -566,12 +649,13 @@ struct FusedWave {
     int n_tiles;
     int lane;
     int base;               // tiles this wave finished in earlier groups (pacing)
+    Mask act[C];            // lanes in range, per chain
 
-    // Tile t, with P = t mod kSmAhead.
-    template <int P>
+    // Tile t, with P = t mod kSmAhead; LAST: t is the last tile.
+    template <int P, bool LAST>
     __device__ __forceinline__ void tile(int t) {
         uint32_t ex[C][4];
-        dec_tile<SPS, C>(ch, tbl, lane, ex);
+        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, act);
         pace(progress, lane, (uint32_t)(base + t), live);
         #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -636,6 +720,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     Seg first[C][kSlots];
     uint16_t st0[C];
     bool act[C];
+    int glanes[G];
     // the loads of the groups gbase .. gbase + G - 1
     auto setup = [&](int64_t gbase) {
         #pragma unroll
@@ -655,6 +740,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             st0[2 * j] = a_st[k0 + lane_ld];
             st0[2 * j + 1] = b_st[k0 + lane_ld];
             act[2 * j] = act[2 * j + 1] = active;
+            glanes[j] = lanes;
             const char* rows[2] = {reinterpret_cast<const char*>(a_sm + k0),
                                    reinterpret_cast<const char*>(b_sm + k0)};
             #pragma unroll
@@ -682,20 +768,26 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
         #pragma unroll
         for (int c = 0; c < C; c++) {
             feed_commit(w.ch.f[c], lane, first[c], w.ch.p[c]);
-            lane_init(w.ch.l[c], act[c], st0[c], L);
+            lane_init(w.ch.l[c], w.ch.f[c], lane, glanes[c / 2], st0[c], L);
+            w.act[c] = __ballot(act[c]);
         }
         w.base = done;
-        int t = 0;
-        for (; t + kSmAhead <= n_tiles; t += kSmAhead) {
-            w.template tile<0>(t);
-            w.template tile<1>(t + 1);
-            w.template tile<2>(t + 2);
-            w.template tile<3>(t + 3);
+        // the first n_tiles - 1 tiles four per iteration, then the last one,
+        // which ends the streams (its variant chosen by tile mod 4)
+        const int body = n_tiles - 1;
+        for (int t = 0; t < body; t += kSmAhead) {
+            w.template tile<0, false>(t);
+            if (t + 1 < body) w.template tile<1, false>(t + 1);
+            if (t + 2 < body) w.template tile<2, false>(t + 2);
+            if (t + 3 < body) w.template tile<3, false>(t + 3);
         }
         static_assert(kSmAhead == 4, "the loop above is unrolled for kSmAhead == 4");
-        if (t < n_tiles) w.template tile<0>(t);
-        if (t + 1 < n_tiles) w.template tile<1>(t + 1);
-        if (t + 2 < n_tiles) w.template tile<2>(t + 2);
+        switch (body % kSmAhead) {
+            case 0: w.template tile<0, true>(body); break;
+            case 1: w.template tile<1, true>(body); break;
+            case 2: w.template tile<2, true>(body); break;
+            default: w.template tile<3, true>(body); break;
+        }
         done += n_tiles;
         g0 += grid_groups;
         if (g0 >= n_groups) break;
@@ -777,17 +869,18 @@ struct DecodeWave {
     int base;               // tiles this wave finished in earlier groups (pacing)
     bool full;              // both groups have 64 lanes in range (wave-uniform)
     bool lines;             // K % 16 == 0: rows start 16-byte aligned
+    Mask act[C];            // lanes in range, per group
+    int last_pairs;         // step pairs of the streams in the last tile
 
     // Tile t (P = t mod kSmAhead) holding n elements per lane (n < 16 only
-    // for a ragged last tile).
-    template <int P>
+    // for a ragged last tile); LAST: t is the last tile.
+    template <int P, bool LAST>
     __device__ __forceinline__ void tile(int t, int n) {
         // A ragged tile is decoded in full: the steps past the lane's last
-        // symbol come after every real one, read zero or stale stream words
-        // and stay inside the table and the ring, and their bytes are not
-        // stored.
+        // symbol come after every real one (no refill checks there), stay
+        // inside the table, and their bytes are not stored.
         uint32_t ex[C][4];
-        dec_tile<SPS, C>(ch, tbl, lane, ex);
+        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, act, last_pairs);
         pace(progress, lane, (uint32_t)(base + t), live);
         uint32_t w[C][4];
         #pragma unroll
@@ -861,15 +954,23 @@ struct DecodeWave {
         }
     }
 
-    // All tiles, four per iteration (the sign/mantissa buffers rotate by
-    // four); the last tile holds n_last elements.
+    // All tiles: the first n_tiles - 1 four per iteration (the sign/mantissa
+    // buffers rotate by four), then the last one, which holds n_last
+    // elements and ends the streams.
     __device__ __forceinline__ void run(int n_last) {
         static_assert(kSmAhead == 4, "the loop below is unrolled for kSmAhead == 4");
-        for (int t = 0; t < n_tiles; t += kSmAhead) {
-            tile<0>(t, t + 1 < n_tiles ? kTile : n_last);
-            if (t + 1 < n_tiles) tile<1>(t + 1, t + 2 < n_tiles ? kTile : n_last);
-            if (t + 2 < n_tiles) tile<2>(t + 2, t + 3 < n_tiles ? kTile : n_last);
-            if (t + 3 < n_tiles) tile<3>(t + 3, t + 4 < n_tiles ? kTile : n_last);
+        const int body = n_tiles - 1;
+        for (int t = 0; t < body; t += kSmAhead) {
+            tile<0, false>(t, kTile);
+            if (t + 1 < body) tile<1, false>(t + 1, kTile);
+            if (t + 2 < body) tile<2, false>(t + 2, kTile);
+            if (t + 3 < body) tile<3, false>(t + 3, kTile);
+        }
+        switch (body % kSmAhead) {
+            case 0: tile<0, true>(body, n_last); break;
+            case 1: tile<1, true>(body, n_last); break;
+            case 2: tile<2, true>(body, n_last); break;
+            default: tile<3, true>(body, n_last); break;
         }
     }
 };
@@ -901,6 +1002,12 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     w.K = K;
     const int rag = (int)(N % kTile);
     w.n_tiles = (int)(N / kTile) + (rag ? 1 : 0);
+    {
+        // step pairs per lane, and those of the last tile
+        constexpr int kPairsPerTile = kTile / SPS / 2;
+        const int64_t pairs = (N / SPS + 1) / 2;
+        w.last_pairs = (int)(pairs - (int64_t)(w.n_tiles - 1) * kPairsPerTile);
+    }
     w.tbl = tbl;
     w.sm_stride = K * 8;
     w.qoff = (uint32_t)(lane & 3) * (uint32_t)K + (uint32_t)(lane >> 2) * 4u;
@@ -951,7 +1058,8 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
         #pragma unroll
         for (int j = 0; j < C; j++) {
             feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
-            lane_init(w.ch.l[j], act[j], st0[j], L);
+            lane_init(w.ch.l[j], w.ch.f[j], lane, w.lanes[j], st0[j], L);
+            w.act[j] = __ballot(act[j]);
         }
         w.base = done;
         w.run(rag ? rag : kTile);
@@ -1005,15 +1113,18 @@ struct GemmWave {
     uint32_t live;
     int64_t sm_stride;
     int n_tiles;
+    int last_pairs;         // step pairs of the streams in the last tile
     int lane;
     float acc[C][NB];
 
-    template <int P>
+    template <int P, bool LAST>
     __device__ __forceinline__ void tile(int t, int n) {
         // a ragged last tile is decoded in full (see DecodeWave::tile) and
-        // its bytes past n are zeroed before they are used
+        // its bytes past n are zeroed before they are used; every lane of a
+        // group is in range (rows are padded to 64)
         uint32_t ex[C][4];
-        dec_tile<SPS, C>(ch, tbl, lane, ex);
+        const Mask all[C] = {~Mask(0), ~Mask(0)};
+        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, all, last_pairs);
         pace(progress, lane, (uint32_t)t, live);
         v2bf wb[C][8];   // bf16 pairs: elements (2m, 2m + 1) of the tile
         #pragma unroll
@@ -1060,13 +1171,21 @@ struct GemmWave {
         }
     }
 
+    // as DecodeWave::run
     __device__ __forceinline__ void run(int n_last) {
         static_assert(kSmAhead == 4, "the loop below is unrolled for kSmAhead == 4");
-        for (int t = 0; t < n_tiles; t += kSmAhead) {
-            tile<0>(t, t + 1 < n_tiles ? kTile : n_last);
-            if (t + 1 < n_tiles) tile<1>(t + 1, t + 2 < n_tiles ? kTile : n_last);
-            if (t + 2 < n_tiles) tile<2>(t + 2, t + 3 < n_tiles ? kTile : n_last);
-            if (t + 3 < n_tiles) tile<3>(t + 3, t + 4 < n_tiles ? kTile : n_last);
+        const int body = n_tiles - 1;
+        for (int t = 0; t < body; t += kSmAhead) {
+            tile<0, false>(t, kTile);
+            if (t + 1 < body) tile<1, false>(t + 1, kTile);
+            if (t + 2 < body) tile<2, false>(t + 2, kTile);
+            if (t + 3 < body) tile<3, false>(t + 3, kTile);
+        }
+        switch (body % kSmAhead) {
+            case 0: tile<0, true>(body, n_last); break;
+            case 1: tile<1, true>(body, n_last); break;
+            case 2: tile<2, true>(body, n_last); break;
+            default: tile<3, true>(body, n_last); break;
         }
     }
 };
@@ -1122,6 +1241,11 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     w.sm_stride = (int64_t)S * Rp * 8;                      // lanes: S * Rp
     const int rag = Nc % kTile;
     w.n_tiles = Nc / kTile + (rag ? 1 : 0);
+    {
+        constexpr int kPairsPerTile = kTile / SPS / 2;
+        const int pairs = (Nc / SPS + 1) / 2;
+        w.last_pairs = pairs - (w.n_tiles - 1) * kPairsPerTile;
+    }
     w.sm_bytes = kLanes * 8u;
     Seg first[CH][kSlots];
     uint16_t st0[CH];
@@ -1160,7 +1284,7 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     #pragma unroll
     for (int j = 0; j < CH; j++) {
         feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
-        lane_init(w.ch.l[j], true, st0[j], L);
+        lane_init(w.ch.l[j], w.ch.f[j], lane, kLanes, st0[j], L);
     }
     w.run(rag ? rag : kTile);
     #pragma unroll
