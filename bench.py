@@ -18,15 +18,19 @@ Prints ONE JSON line (progress goes to stderr):
                 fused kernel's 256)
   roofline      compressed HBM bytes of one fused launch / its duration
                 (HIP events around each launch on the launch stream)
+  ceiling       what the raw add's launch shape streams with the arithmetic
+                taken out (read-only, write-only, 2:1 read/write), the raw
+                add's rate as a fraction of the 2:1 ceiling and of 8 TB/s
   decode        config 2: gpu_tans_decode of 2^30 elements (Gaussian and
                 Laplace data, nibble and pair tables), GB/s and bits/byte
   cpu_baseline  the reference's CPU path (the C restatement in oracle/) on a
                 bounded sample of the same workload
 
     python bench.py [--gpus 1] [--steps 200] [--warmup 20]
-    python bench.py --profile fused|raw|memcpy|decode|gemv|gemv_raw|encode
-                    [--alphabet pair|nibble] --steps 5
-                                  # one kernel (or the encoder's passes) only, for rocprofv3
+    python bench.py --profile fused|raw|memcpy|read|write|stream21|decode|gemv|gemv_raw|
+                              gemm|encode  [--alphabet pair|nibble] [--batch B] --steps 5
+                                  # one kernel (or the encoder's passes, or one 40-layer
+                                  # GEMM pass) only, for rocprofv3
 """
 from __future__ import annotations
 
@@ -69,9 +73,13 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-gemm", action="store_true", help="skip configs 3-4 (decode-GEMV/GEMM)")
     p.add_argument("--alphabet", choices=("pair", "nibble"), default="pair",
                    help="alphabet of --profile fused/decode")
-    p.add_argument("--profile", choices=("fused", "raw", "memcpy", "decode", "gemv", "gemv_raw",
+    p.add_argument("--profile", choices=("fused", "raw", "memcpy", "read", "write", "stream21",
+                                         "decode", "gemv", "gemv_raw", "gemm", "gemm_raw",
                                          "encode"),
                    help="only launch this kernel --steps times (for rocprofv3)")
+    p.add_argument("--policy", choices=("nt", "default"), default="nt",
+                   help="load/store policy of --profile read/write/stream21")
+    p.add_argument("--batch", type=int, default=1, help="batch of --profile gemm/gemm_raw")
     return p.parse_args()
 
 
@@ -322,16 +330,12 @@ def run_gemv_config(seed: int, steps: int, warmup: int, settle_s: float) -> dict
     return out
 
 
-def run_gemm_config(seed: int, batches, steps: int, warmup: int, settle_s: float) -> dict:
-    """Config 4: GEMM_LAYERS layers of W_up [17408, 5120] and W_down
-    [5120, 17408]; per layer h = W_up x, y = W_down h for X bf16 [B, 5120].
-    Layers in the second half are encoded with a table from a
-    Laplace(0, 0.015) histogram (mismatched to their Gaussian data).  A pass
-    over all layers is one HIP graph."""
-    import torch
-    import rans_vectoradd as R
+def gemm_layers(seed: int):
+    """Config 4's GEMM_LAYERS layers of (W_up [17408, 5120], W_down
+    [5120, 17408]) as gemm_matrix tuples.  Layers in the second half are
+    encoded with a table from a Laplace(0, 0.015) histogram (mismatched to
+    their Gaussian data)."""
     from rans_vectoradd import data as D
-
     lap, _ = D.laplace_fp8_bytes(1 << 24, seed=seed + 7)
     lap_hist = D.exp_histogram(lap)
     rows, cols = GEMM_UP
@@ -341,49 +345,112 @@ def run_gemm_config(seed: int, batches, steps: int, warmup: int, settle_s: float
         up = gemm_matrix(rows, cols, seed + 1000 + 2 * i, hist)
         down = gemm_matrix(cols, rows, seed + 1001 + 2 * i, hist)
         layers.append((up, down))
+    return layers
+
+
+def gemm_x(seed: int, B: int):
+    import torch
+    gx = torch.Generator(device="cuda").manual_seed(seed + B)
+    return torch.randn(B, GEMM_UP[1], generator=gx, device="cuda").to(torch.bfloat16)
+
+
+def gemm_pass(layers, X, fused: bool):
+    """One pass over `layers`: per layer h = W_up x, y = W_down h (fused
+    decode-GEMM or the uncompressed FP8 kernel); returns the stacked y."""
+    import torch
+    import rans_vectoradd as R
+
+    def run():
+        outs = []
+        for (wu, su, mu, tu), (wd, sd, md, td) in layers:
+            if fused:
+                h = R.fp8_gemm_fused_tans(mu, tu, X, su)
+                outs.append(R.fp8_gemm_fused_tans(md, td, h, sd))
+            else:
+                h = R.fp8_gemm_raw(wu, X, su)
+                outs.append(R.fp8_gemm_raw(wd, h, sd))
+        return torch.stack(outs)
+    return run
+
+
+def run_gemm_config(seed: int, batches, steps: int, warmup: int, settle_s: float) -> dict:
+    """Config 4: a pass over GEMM_LAYERS layers (gemm_layers) for X bf16
+    [B, 5120], each pass one HIP graph; the matched-table and
+    mismatched-table halves are also timed as passes of their own.
+    Roofline bytes: the encoded weights (or the FP8 weights for the raw
+    kernel) plus activations in and out."""
+    import torch
+
+    rows, cols = GEMM_UP
+    layers = gemm_layers(seed)
     half = GEMM_LAYERS // 2
 
-    def bits(ls):
-        b = sum(u[2].compressed_bytes() + d[2].compressed_bytes() for u, d in ls)
-        return b * 8 / (len(ls) * 2 * rows * cols)
+    def comp_bytes(ls):
+        return sum(u[2].compressed_bytes() + d[2].compressed_bytes() for u, d in ls)
 
-    comp = sum(u[2].compressed_bytes() + d[2].compressed_bytes() for u, d in layers)
+    def bits(ls):
+        return comp_bytes(ls) * 8 / (len(ls) * 2 * rows * cols)
+
+    comp = comp_bytes(layers)
     raw_bytes = GEMM_LAYERS * 2 * rows * cols
     res = {"layers": GEMM_LAYERS, "shapes": [[rows, cols], [cols, rows]],
            "bits_per_byte_matched": bits(layers[:half]),
            "bits_per_byte_mismatched": bits(layers[half:]), "batches": []}
+    reps = max(steps // 10, 5)
     for B in batches:
-        gx = torch.Generator(device="cuda").manual_seed(seed + B)
-        X = torch.randn(B, cols, generator=gx, device="cuda").to(torch.bfloat16)
-
-        def fused_pass(layers=layers, X=X):
-            outs = []
-            for (wu, su, mu, tu), (wd, sd, md, td) in layers:
-                h = R.fp8_gemm_fused_tans(mu, tu, X, su)
-                outs.append(R.fp8_gemm_fused_tans(md, td, h, sd))
-            return torch.stack(outs)
-
-        def raw_pass(layers=layers, X=X):
-            outs = []
-            for (wu, su, mu, tu), (wd, sd, md, td) in layers:
-                h = R.fp8_gemm_raw(wu, X, su)
-                outs.append(R.fp8_gemm_raw(wd, h, sd))
-            return torch.stack(outs)
-
+        X = gemm_x(seed, B)
+        io = GEMM_LAYERS * B * 2 * (2 * cols + 2 * rows)     # bf16 x, h in; h, y out
+        fused_pass, raw_pass = gemm_pass(layers, X, True), gemm_pass(layers, X, False)
         yf, yr = fused_pass().float(), raw_pass().float()
         rel = float(((yf - yr).abs().amax(dim=(1, 2)) / yr.abs().amax(dim=(1, 2))).max())
-        f_ms, f_step, f_same = graph_timed(fused_pass, 1, max(steps // 10, 5), 2, settle_s)
-        r_ms, r_step, r_same = graph_timed(raw_pass, 1, max(steps // 10, 5), 2, settle_s)
+        f_ms, f_step, f_same = graph_timed(fused_pass, 1, reps, 2, settle_s)
+        r_ms, r_step, r_same = graph_timed(raw_pass, 1, reps, 2, settle_s)
+        halves = {}
+        for name, ls in (("matched", layers[:half]), ("mismatched", layers[half:])):
+            _, h_step, h_same = graph_timed(gemm_pass(ls, X, True), 1, reps, 2, settle_s)
+            h_bytes = comp_bytes(ls) + io // 2
+            halves[name] = {"fused_ms_per_half_pass": h_step, "bits_per_byte": bits(ls),
+                            "x_raw": (r_step / 2) / h_step,
+                            "hbm_gbs": h_bytes / (h_step * 1e-3) / 1e9,
+                            "graph_replays_match_eager": h_same}
+        f_gbs = (comp + io) / (f_step * 1e-3) / 1e9
+        r_gbs = (raw_bytes + io) / (r_step * 1e-3) / 1e9
         res["batches"].append({
             "batch": B, "fused_ms_per_pass": f_step, "raw_ms_per_pass": r_step,
-            "x_raw": r_step / f_step, "fused_hbm_gbs": comp / (f_step * 1e-3) / 1e9,
-            "raw_hbm_gbs": raw_bytes / (r_step * 1e-3) / 1e9, "max_rel_diff_vs_raw": rel,
+            "x_raw": r_step / f_step, "fused_hbm_gbs": f_gbs, "raw_hbm_gbs": r_gbs,
+            "fused_frac_of_peak": f_gbs / HBM_PEAK_GBS, "raw_frac_of_peak": r_gbs / HBM_PEAK_GBS,
+            "halves": halves, "max_rel_diff_vs_raw": rel,
             "graph_replays_match_eager": f_same and r_same})
         log(f"  gemm B={B}: fused {f_step:.3f} ms  raw {r_step:.3f} ms  x_raw "
-            f"{r_step / f_step:.3f}  rel diff {rel:.2e}")
+            f"{r_step / f_step:.3f}  matched/mismatched half {halves['matched']['fused_ms_per_half_pass']:.3f}"
+            f"/{halves['mismatched']['fused_ms_per_half_pass']:.3f} ms  rel diff {rel:.2e}")
     del layers
     torch.cuda.empty_cache()
     return res
+
+
+def run_ceilings(qa, qb, steps: int, warmup: int, settle_s: float) -> dict:
+    """What fp8_vecadd_raw's launch shape streams with the arithmetic taken
+    out: read-only, write-only and 2:1 read/write (c = a ^ b) over the
+    config-1 vectors, with non-temporal and default load/store policies."""
+    import torch
+    from rans_vectoradd import _C as C
+
+    buf = torch.empty_like(qa)
+    n = qa.numel()
+    cases = {"read": (lambda nt: lambda: C.stream_probe("read", qa, nontemporal=nt), n),
+             "write": (lambda nt: lambda: C.stream_probe("write", out=buf, nontemporal=nt), n),
+             "stream21": (lambda nt: lambda: C.stream_probe("stream21", qa, qb, out=buf,
+                                                             nontemporal=nt), 3 * n)}
+    out = {}
+    for name, (mk, nbytes) in cases.items():
+        for pol, nt in (("nt", True), ("default", False)):
+            k_ms, s_ms = timed(mk(nt), steps, warmup, settle_s)
+            out[f"{name}_{pol}"] = {"bytes": nbytes, "kernel_ms": k_ms, "step_ms": s_ms,
+                                    "gbs": nbytes / (s_ms * 1e-3) / 1e9}
+    out["stream21_exact"] = bool(torch.equal(buf, qa ^ qb))   # the last run wrote a ^ b
+    del buf
+    return out
 
 
 def read_traffic():
@@ -498,7 +565,7 @@ def profile_only(args) -> None:
     the timed part, for rocprofv3 runs."""
     import torch
     import rans_vectoradd as R
-    from rans_vectoradd import tans_codec as T
+    from rans_vectoradd import _C as C, tans_codec as T
 
     if args.profile in ("gemv", "gemv_raw"):   # config 3, one W (it stays MALL-resident)
         gx = torch.Generator(device="cuda").manual_seed(args.seed + 99)
@@ -522,12 +589,24 @@ def profile_only(args) -> None:
                          alphabet=args.alphabet)
         del q
         fn = lambda: R.gpu_tans_decode(d[0], d[2], d[1], d[3], d[4], d[6], d[5], HEADLINE_LANE)  # noqa
+    elif args.profile in ("gemm", "gemm_raw"):   # config 4: one 40-layer pass at --batch
+        layers = gemm_layers(args.seed)
+        X = gemm_x(args.seed, args.batch)
+        fn = gemm_pass(layers, X, args.profile == "gemm")
     else:
         qa, qb, hist = make_inputs(args.seed)
+        buf = torch.empty_like(qa)
+        nt = args.policy == "nt"
         if args.profile == "raw":
             fn = lambda: R.fp8_vecadd_raw(qa, qb)   # noqa: E731
         elif args.profile == "memcpy":
             fn = lambda: R.fp8_memcpy(qa)           # noqa: E731
+        elif args.profile == "read":
+            fn = lambda: C.stream_probe("read", qa, nontemporal=nt)   # noqa: E731
+        elif args.profile == "write":
+            fn = lambda: C.stream_probe("write", out=buf, nontemporal=nt)   # noqa: E731
+        elif args.profile == "stream21":
+            fn = lambda: C.stream_probe("stream21", qa, qb, out=buf, nontemporal=nt)   # noqa: E731
         else:
             dev_args, _, _ = encode_pair(qa, qb, hist, HEADLINE_LANE, args.alphabet)
             fn = lambda: R.fp8_vecadd_fused_tans(*dev_args, HEADLINE_LANE)   # noqa: E731
@@ -562,6 +641,12 @@ def main() -> None:
                                  args.settle)
     cpy_kernel, cpy_step = timed(lambda: R.fp8_memcpy(qa), args.steps, args.warmup,
                                  args.settle)
+    log("streaming ceilings")
+    ceil = run_ceilings(qa, qb, args.steps, args.warmup, args.settle)
+    raw_gbs = 3 * N_ELEMS / (raw_step * 1e-3) / 1e9
+    best21 = max(ceil["stream21_nt"]["gbs"], ceil["stream21_default"]["gbs"])
+    log("  " + "  ".join(f"{k} {v['gbs']:.0f}" for k, v in ceil.items() if isinstance(v, dict))
+        + f" GB/s; raw {raw_gbs:.0f} GB/s = {raw_gbs / best21:.3f} of the 2:1 ceiling")
 
     configs = [(HEADLINE_LANE, "pair")]
     if not args.no_sweep:
@@ -601,9 +686,10 @@ def main() -> None:
         "exact_vs_raw": head["exact_vs_raw"],
         "kernel_ms": head["kernel_ms"],
         "compressed_hbm_gbs": achieved,
-        "raw": {"kernel_ms": raw_kernel, "step_ms": raw_step,
-                "gbs": 3 * N_ELEMS / (raw_step * 1e-3) / 1e9,
-                "frac_of_peak": 3 * N_ELEMS / (raw_step * 1e-3) / 1e9 / HBM_PEAK_GBS},
+        "raw": {"kernel_ms": raw_kernel, "step_ms": raw_step, "gbs": raw_gbs,
+                "frac_of_peak": raw_gbs / HBM_PEAK_GBS,
+                "frac_of_2to1_ceiling": raw_gbs / best21},
+        "ceiling": ceil | {"best_2to1_gbs": best21, "best_2to1_frac_of_peak": best21 / HBM_PEAK_GBS},
         "memcpy": {"kernel_ms": cpy_kernel, "step_ms": cpy_step,
                    "gbs": 2 * N_ELEMS / (cpy_step * 1e-3) / 1e9},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,

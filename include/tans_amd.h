@@ -123,6 +123,17 @@ int tans_fp8_memcpy(const void* a, void* c, int64_t n, void* stream);
 int tans_fp8_vecadd_raw(const void* a, const void* b, void* c, int64_t n,
                         void* stream);
 
+/* Bandwidth probes at tans_fp8_vecadd_raw's launch shape with the arithmetic
+ * taken out; no counterpart in the reference, whose fp8_memcpy
+ * (csrc/fp8_memcpy.cu:45-64, "practical bandwidth ceiling" at :71-73) is
+ * the one ceiling it measures.  mode 0 reads A (n bytes), mode 1 writes C,
+ * mode 2 writes C = A xor B (the raw add's two reads per write).
+ * nontemporal != 0 uses non-temporal loads and stores (the raw add's
+ * policy).  Mode 0 may store 4 bytes to sink.  n % 16 == 0; buffers a mode
+ * does not use may be NULL.                                             */
+int tans_stream_probe(int32_t mode, int32_t nontemporal, const void* a, const void* b,
+                      void* c, int64_t n, void* sink, void* stream);
+
 /* Device decode table from device spread/freqs (no host round trip).
  * Same output as tans_build_decode_table.                               */
 int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs,

@@ -14,7 +14,9 @@ Pure-numpy restatements of the reference's Python table builders:
                           rans_vectoradd/tans_codec.py:109-124
 
 plus ctypes bindings of ``oracle.c`` (FP8 add, reference-format codec, and the
-wave64-layout checker).
+wave64-layout checker), and of ``_ref/libref_codec.so`` where it is built: the
+reference's own CPU encoder (csrc/tans_codec.cpp), compiled unmodified from the
+reference tree (``make -C oracle ref``), the checker of ``ref_encode``.
 """
 from __future__ import annotations
 
@@ -65,6 +67,67 @@ def lib() -> ctypes.CDLL:
         _lib.ora_w64_decode.restype = I
         _lib.ora_w64_decode.argtypes = [P, P, P, P, P, P, I, I, I, I64, I64, P]
     return _lib
+
+
+REF_LIB_PATH = os.path.join(_HERE, "_ref", "libref_codec.so")
+_ref_lib = None
+
+
+def build_ref(ref_csrc: str = "/root/reference/csrc") -> bool:
+    """Compile the reference's csrc/tans_codec.cpp with ref_harness.cpp into
+    _ref/libref_codec.so when the reference tree is present; True if built."""
+    if not os.path.exists(os.path.join(ref_csrc, "tans_codec.cpp")):
+        return False
+    subprocess.run(["make", "-s", "-C", _HERE, "ref", f"REF={ref_csrc}"], check=True)
+    return True
+
+
+def ref_lib():
+    """The compiled reference encoder, or None where it is not built."""
+    global _ref_lib
+    if _ref_lib is None and os.path.exists(REF_LIB_PATH):
+        import torch  # noqa: F401  (loads libtorch's libraries the encoder links)
+        lib_ = ctypes.CDLL(REF_LIB_PATH)
+        P, I64 = ctypes.c_void_p, ctypes.c_int64
+        lib_.ref_encode.restype = P
+        lib_.ref_encode.argtypes = [P, I64, I64, P, I64, P, I64, ctypes.POINTER(I64),
+                                    ctypes.POINTER(I64)]
+        lib_.ref_encode_copy.restype = None
+        lib_.ref_encode_copy.argtypes = [P, P, P, P, P]
+        lib_.ref_encode_free.restype = None
+        lib_.ref_encode_free.argtypes = [P]
+        lib_.ref_last_error.restype = ctypes.c_char_p
+        lib_.ref_last_error.argtypes = []
+        _ref_lib = lib_
+    return _ref_lib
+
+
+def reference_encode(symbols: np.ndarray, freqs, spread):
+    """The reference's tans_encode_interleaved (csrc/tans_codec.cpp:69-196)
+    itself -> (compressed u8, states u16[K], offsets i32, partial u8[K]);
+    raises RuntimeError with the reference's message where it rejects the
+    input."""
+    lib_ = ref_lib()
+    if lib_ is None:
+        raise RuntimeError(f"{REF_LIB_PATH} is not built")
+    symbols = np.ascontiguousarray(symbols, dtype=np.uint8)
+    freqs = np.ascontiguousarray(freqs, dtype=np.int32)
+    spread = np.ascontiguousarray(spread, dtype=np.int32)
+    K, N = symbols.shape
+    nb, no = ctypes.c_int64(), ctypes.c_int64()
+    h = lib_.ref_encode(_p(symbols), K, N, _p(freqs), freqs.size, _p(spread), spread.size,
+                        ctypes.byref(nb), ctypes.byref(no))
+    if not h:
+        raise RuntimeError(lib_.ref_last_error().decode(errors="replace"))
+    try:
+        comp = np.empty(nb.value, np.uint8)
+        states = np.empty(K, np.uint16)
+        offsets = np.empty(no.value, np.int32)
+        partial = np.empty(K, np.uint8)
+        lib_.ref_encode_copy(h, _p(comp), _p(states), _p(offsets), _p(partial))
+    finally:
+        lib_.ref_encode_free(h)
+    return comp, states, offsets, partial
 
 
 def _p(a: np.ndarray) -> ctypes.c_void_p:

@@ -5,6 +5,8 @@
 //   fp8_copy_kernel          16-byte streaming copy, the HBM ceiling
 //                            (role of csrc/fp8_memcpy.cu:30-41)
 //   fp8_add_kernel           uncompressed FP8 add (csrc/vecadd.cu:41-73)
+//   stream_probe_kernel      read-only / write-only / 2:1 streaming at the
+//                            add's launch shape (bandwidth ceilings)
 //   table_kernel             decode table from device spread/freqs
 //                            (csrc/tans_decode.cu:23-59 without the host trip)
 //   fused_add_kernel<SPS,G>  decode two encodings + FP8 add
@@ -140,6 +142,31 @@ __global__ __launch_bounds__(kBlock) void fp8_add_kernel(const v4u* __restrict__
         const v4u va = __builtin_nontemporal_load(a + i);
         const v4u vb = __builtin_nontemporal_load(b + i);
         __builtin_nontemporal_store(add16_fp8(va, vb), c + i);
+    }
+}
+
+// Bandwidth probes: the same launch shape with the arithmetic taken out, to
+// measure what this shape can stream.  MODE 0 reads a (a load whose XOR
+// matches a fixed key stores its index to sink, which keeps the loads
+// live); MODE 1 writes c; MODE 2 writes c = a ^ b (the raw add's 2:1 mix).
+template <int MODE, bool NT>
+__global__ __launch_bounds__(kBlock) void stream_probe_kernel(const v4u* __restrict__ a,
+                                                              const v4u* __restrict__ b,
+                                                              v4u* __restrict__ c, int64_t n_vec,
+                                                              uint32_t* __restrict__ sink) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n_vec) return;
+    if constexpr (MODE == 0) {
+        const v4u v = NT ? __builtin_nontemporal_load(a + i) : a[i];
+        if ((v.x ^ v.y ^ v.z ^ v.w) == 0x9E3779B9u) sink[0] = (uint32_t)i;
+    } else if constexpr (MODE == 1) {
+        const uint32_t x = (uint32_t)i;
+        const v4u v = {x, x ^ 0x55555555u, x ^ 0xAAAAAAAAu, ~x};
+        if (NT) __builtin_nontemporal_store(v, c + i); else c[i] = v;
+    } else {
+        const v4u v = NT ? __builtin_nontemporal_load(a + i) ^ __builtin_nontemporal_load(b + i)
+                         : a[i] ^ b[i];
+        if (NT) __builtin_nontemporal_store(v, c + i); else c[i] = v;
     }
 }
 
@@ -1499,6 +1526,34 @@ int tans_fp8_vecadd_raw(const void* a, const void* b, void* c, int64_t n, void* 
     hipLaunchKernelGGL(fp8_add_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream,
                        (const v4u*)a, (const v4u*)b, (v4u*)c, n_vec);
     return hip_check(hipGetLastError(), "fp8_add_kernel launch");
+}
+
+int tans_stream_probe(int32_t mode, int32_t nontemporal, const void* a, const void* b, void* c,
+                      int64_t n, void* sink, void* stream) {
+    if (mode < 0 || mode > 2) return fail(TANS_EINVAL, "stream_probe: mode must be 0, 1 or 2");
+    if (n < 0 || n % 16) return fail(TANS_EINVAL, "stream_probe: n must be a multiple of 16");
+    if (n == 0) return TANS_OK;
+    const bool need_a = mode != 1, need_b = mode == 2, need_c = mode != 0;
+    if ((need_a && !a) || (need_b && !b) || (need_c && !c) || (mode == 0 && !sink))
+        return fail(TANS_EINVAL, "stream_probe: null pointer");
+    if ((need_a && !aligned(a, 16)) || (need_b && !aligned(b, 16)) || (need_c && !aligned(c, 16)) ||
+        (mode == 0 && !aligned(sink, 4)))
+        return fail(TANS_EINVAL, "stream_probe: buffers must be 16-byte aligned");
+    const int64_t n_vec = n / 16;
+    const dim3 grid((unsigned)((n_vec + kBlock - 1) / kBlock));
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, (hipStream_t)stream, (const v4u*)a,
+                           (const v4u*)b, (v4u*)c, n_vec, (uint32_t*)sink);
+    };
+    switch (mode * 2 + (nontemporal ? 1 : 0)) {
+        case 0: launch(stream_probe_kernel<0, false>); break;
+        case 1: launch(stream_probe_kernel<0, true>); break;
+        case 2: launch(stream_probe_kernel<1, false>); break;
+        case 3: launch(stream_probe_kernel<1, true>); break;
+        case 4: launch(stream_probe_kernel<2, false>); break;
+        default: launch(stream_probe_kernel<2, true>); break;
+    }
+    return hip_check(hipGetLastError(), "stream_probe_kernel launch");
 }
 
 int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs, int32_t nsym,

@@ -182,6 +182,41 @@ def fp8_vecadd_raw(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     return C
 
 
+_PROBE_MODES = {"read": 0, "write": 1, "stream21": 2}
+
+
+def stream_probe(mode: str, A: torch.Tensor | None = None, B: torch.Tensor | None = None,
+                 out: torch.Tensor | None = None, nontemporal: bool = True) -> torch.Tensor | None:
+    """Bandwidth probe at fp8_vecadd_raw's launch shape, no arithmetic
+    (no reference counterpart; its fp8_memcpy is the one ceiling it
+    measures).  "read": reads A; "write": writes `out`; "stream21": writes
+    out = A ^ B.  Returns `out` (allocated like A when not given) or None
+    for "read"."""
+    _require(mode in _PROBE_MODES, f"mode must be one of {sorted(_PROBE_MODES)}")
+    m = _PROBE_MODES[mode]
+    if m != 1:
+        _check_dev("A", A, torch.uint8)
+    if m == 2:
+        _check_dev("B", B, torch.uint8)
+        _require(A.numel() == B.numel() and A.device == B.device, "A and B must match")
+    if m != 0:
+        if out is None:
+            _require(A is not None, "write needs `out` or A to size it")
+            out = torch.empty_like(A)
+        _check_dev("out", out, torch.uint8)
+    ref = A if A is not None else out
+    n = ref.numel()
+    _require(n % 16 == 0, "length must be a multiple of 16")
+    with _on(ref.device):
+        sink = torch.empty(1, dtype=torch.int32, device=ref.device) if m == 0 else None
+        check(lib.tans_stream_probe(m, int(bool(nontemporal)), _ptr(A) if m != 1 else None,
+                                    _ptr(B) if m == 2 else None,
+                                    _ptr(out) if m != 0 else None, n,
+                                    _ptr(sink) if m == 0 else None, _stream(ref.device)),
+              "stream_probe")
+    return out if m != 0 else None
+
+
 def fp8_vecadd_fused_tans(a_comp: torch.Tensor, a_offsets: torch.Tensor, a_states: torch.Tensor,
                           a_partial: torch.Tensor, a_sm: torch.Tensor,
                           b_comp: torch.Tensor, b_offsets: torch.Tensor, b_states: torch.Tensor,

@@ -52,6 +52,12 @@ def test_gpu_entry_points_validate_before_launch():
     assert lib.tans_decode(dummy, 1024, dummy, dummy, dummy, dummy, 12, 64, 3, dummy, None) == -1
     assert lib.tans_decode(dummy, 1024, dummy, dummy, dummy, dummy, 12, 0, 16, dummy, None) == 0
     assert lib.tans_build_decode_table_device(dummy, dummy, 16, 12, dummy, None) == -1
+    assert lib.tans_stream_probe(3, 1, dummy, dummy, dummy, 16, dummy, None) == -1
+    assert b"mode" in lib.tans_last_error()
+    assert lib.tans_stream_probe(2, 1, dummy, None, dummy, 16, None, None) == -1
+    assert lib.tans_stream_probe(0, 1, dummy, None, None, 16, None, None) == -1    # no sink
+    assert lib.tans_stream_probe(1, 0, None, None, dummy, 24, None, None) == -1
+    assert lib.tans_stream_probe(1, 0, None, None, None, 0, None, None) == 0
 
 
 def test_python_api_rejects_cpu_and_mismatched_tensors():

@@ -45,6 +45,25 @@ def test_memcpy(R):
     assert torch.equal(R.fp8_memcpy(x), x)
 
 
+@pytest.mark.parametrize("nontemporal", [True, False])
+def test_stream_probes(R, nontemporal):
+    """The bandwidth probes move the bytes they claim: 2:1 writes a ^ b,
+    write-only writes its index pattern, read-only runs without error."""
+    from rans_vectoradd import _C as C
+    n = (1 << 20) + 16
+    _say(f"case: stream_probe n={n} nt={nontemporal}")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    a = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=g)
+    b = torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda", generator=g)
+    assert torch.equal(C.stream_probe("stream21", a, b, nontemporal=nontemporal), a ^ b)
+    w = C.stream_probe("write", out=torch.zeros_like(a), nontemporal=nontemporal)
+    i = torch.arange(n // 16, dtype=torch.int64, device="cuda")
+    words = torch.stack([i, i ^ 0x55555555, i ^ 0xAAAAAAAA, i ^ 0xFFFFFFFF], dim=1)
+    assert torch.equal(w.view(torch.int32).view(-1, 4).long() & 0xFFFFFFFF, words)
+    assert C.stream_probe("read", a, nontemporal=nontemporal) is None
+    torch.cuda.synchronize()
+
+
 def test_raw_ragged_sizes(R, lut):
     for n in (16, 4096 + 16, 1 << 16):
         _say(f"case: fp8_vecadd_raw n={n}")
