@@ -190,13 +190,17 @@ int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* work
 /* y[b][r] = bf16(scale * sum_c W[r][c] * x[b][c]), fp32 accumulation,
  * round-to-nearest-even to bf16; W is R x C FP8 E4M3FN, tANS-coded as
  * written by rans_vectoradd.tans_codec.encode_matrix: rows padded to
- * Rp = R rounded up to 64, columns cut into S segments of Nc (even,
- * <= 512) columns with (S - 1) * Nc < C <= S * Nc, lane s * Rp + r holding
- * row r of segment s; comp/offsets/states/sm are that encoding (K = S * Rp
- * lanes of Nc elements) and table its decode table.
+ * Rp = R rounded up to 64, columns cut into S segments of Nc columns (a
+ * multiple of 32, <= 1024) with (S - 1) * Nc < C <= S * Nc.  Lane
+ * ((s * Rp / 16 + g) * 4 + q) * 16 + r holds row 16 g + r of segment s:
+ * of each 64-column block of the segment, columns 16 q .. 16 q + 15, and
+ * of a last block of 32 columns, columns 8 q .. 8 q + 7 (padding bytes
+ * are multiplied by zero).  comp/offsets/states/sm are that encoding
+ * (K = 4 * S * Rp lanes of Nc / 4 elements) and table its decode table.
  *   x          bf16 [B, C], 1 <= B <= 8
- *   workspace  device memory of at least S * B * Rp * 4 bytes (per-segment
- *              fp32 partial sums; contents on entry do not matter)
+ *   workspace  device memory of at least S * B * Rp * 4 bytes, 16-byte
+ *              aligned (per-segment fp32 partial sums; contents on entry
+ *              do not matter)
  *   y          bf16 [B, R]
  * Partial sums are added in a fixed order, so results are deterministic. */
 int tans_fp8_gemm_fused(const void* comp, int64_t comp_bytes, const int64_t* offsets,

@@ -13,10 +13,11 @@
 //                            (csrc/vecadd.cu:156-243)
 //   decode_kernel<SPS>       decode to FP8 bytes [N, K]
 //                            (csrc/tans_decode.cu:125-155)
-//   gemm_fused_kernel<SPS,B> decode W + skinny GEMM partial sums (no
-//                            counterpart in the reference), with
-//                            gemm_finalize_kernel and the uncompressed
-//                            baseline gemm_raw_kernel<B>
+//   gemm_fused_kernel<SPS>   decode W + skinny GEMM partial sums on the
+//                            matrix cores (no counterpart in the
+//                            reference), with gemm_finalize_kernel and the
+//                            uncompressed baselines gemm_raw_dot2_kernel
+//                            (B = 1) and gemm_raw_kernel (B >= 2)
 //
 // Decoder design.  One wave64 decodes one 64-lane group; each lane owns one
 // tANS state.  The decode table lives in LDS as 8-byte entries addressed by
@@ -1099,35 +1100,57 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
 
 // ---------------------------------------------------------------------
 // Fused decode + skinny GEMM: y[b][r] = scale * sum_c W[r][c] * x[b][c]
-// with W tANS-coded and B <= 8 rows of bf16 x.
+// with W tANS-coded and B <= 8 rows of bf16 x, on the matrix cores.
 //
 // Encoding (rans_vectoradd.tans_codec.encode_matrix): W, padded to Rp rows
-// (a multiple of 64) and S * Nc columns, is cut into S column segments of
-// Nc columns; lane s * Rp + r holds row r of segment s, so a group is 64
-// rows of one segment and every lane of a wave works on the same columns.
+// (a multiple of 64) and S * Nc columns (Nc a multiple of 32), is cut into
+// S column segments of Nc columns.  A group is 16 rows of one segment:
+// lane j = 16 q + r holds row r of the group and, of every 64-column block
+// of the segment, the 16 columns 16 q .. 16 q + 15 (a last block of 32
+// columns: the 8 columns 8 q .. 8 q + 7).  So one tile of a lane (16
+// elements) is exactly what v_mfma_f32_16x16x32_bf16 takes from that lane
+// as its A operand, split in two k-blocks of 8: the wave's 64 lanes hold a
+// 16-row x 64-column block of W.  x comes from an LDS stage of the
+// segment's columns (zero past the segment or the matrix), as the B
+// operand: lane j reads x[j % 16][the same 8 columns] (lanes j % 16 >= B
+// read a row whose products are never stored).  The 4 fp32 accumulators of
+// lane j hold rows 4 (j / 16) .. 4 (j / 16) + 3 of the group for batch row
+// j % 16.  The batch size does not change the work per tile.
 //
 // A workgroup takes one segment and up to 32 row groups (two per wave, two
-// chains per lane).  It stages the segment's x columns in LDS (zero past
-// the matrix and past the segment), and each tile's 16 FP8 weights per
-// lane become 8 bf16 pairs (exact) that meet x in v_dot2_f32_bf16 with
-// fp32 accumulation; x is read once per tile and batch row with a
-// wave-uniform LDS address (a broadcast).  Partial sums go to a workspace
-// [S][B][Rp] and gemm_finalize_kernel adds the S segments in a fixed
-// order, scales and rounds to bf16 (round to nearest even).
+// chains per lane).  Partial sums go to a workspace [S][B][Rp] and
+// gemm_finalize_kernel adds the S segments in a fixed order, scales and
+// rounds to bf16 (round to nearest even).
 // ---------------------------------------------------------------------
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kGemmChains = 2;                        // row groups per wave
+constexpr int kGemmGroupRows = 16;                    // rows of a group
 constexpr int kGemmGroupsPerBlock = kDecWaves * kGemmChains;
 constexpr int kGemmMaxBatch = 8;
-constexpr int kGemmMaxSegCols = 512;                  // Nc limit: the x stage is 8 KiB
+constexpr int kGemmMaxSegCols = 1024;                 // Nc limit
+constexpr int kGemmXStride = kGemmMaxSegCols + 16;    // bf16 per x stage row (32 bytes of pad)
+static_assert(kGemmMaxSegCols == kDecBlock, "one x stage column per thread");
 
 template <int SPS>
 struct GemmSmem {
     DecSmem<SPS, kGemmChains> dec;
-    uint32_t xs[kGemmMaxBatch * kGemmMaxSegCols / 2];  // bf16 pairs [B][kGemmMaxSegCols / 2]
+    alignas(16) __bf16 xs[kGemmMaxBatch][kGemmXStride];   // x columns of the segment
 };
+static_assert(sizeof(GemmSmem<2>) <= 160 * 1024 && sizeof(GemmSmem<1>) <= 160 * 1024,
+              "the GEMM workgroup's LDS fits one CU");
 
-template <int SPS, int NB>
+// Four bf16 pairs from 4 FP8 words (exact: every E4M3FN value is a bf16).
+__device__ __forceinline__ v8bf fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
+    const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false);
+    const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true);
+    const v2bf p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false);
+    const v2bf p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true);
+    return v8bf{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+template <int SPS>
 struct GemmWave {
     static constexpr int C = kGemmChains;
     Chains<C> ch;
@@ -1135,55 +1158,41 @@ struct GemmWave {
     const char* pf[C];
     uint32_t sm_bytes;
     const v2u* tbl;
-    const uint32_t* xs;     // LDS x stage of the segment
+    const __bf16* xrow;     // this lane's x stage row
     uint32_t* progress;
     uint32_t live;
     int64_t sm_stride;
     int n_tiles;
     int last_pairs;         // step pairs of the streams in the last tile
     int lane;
-    float acc[C][NB];
+    int q;                  // lane / 16: the lane's column chunk
+    v4f acc[C];
 
     template <int P, bool LAST>
     __device__ __forceinline__ void tile(int t, int n) {
-        // a ragged last tile is decoded in full (see DecodeWave::tile) and
-        // its bytes past n are zeroed before they are used; every lane of a
-        // group is in range (rows are padded to 64)
+        // a half last tile (n = 8) is decoded in full (see DecodeWave::tile)
+        // and its bytes past n are zeroed; every lane of a group is in range
+        // (rows are padded to 64)
         uint32_t ex[C][4];
         const Mask all[C] = {~Mask(0), ~Mask(0)};
         dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, all, last_pairs);
         pace(progress, lane, (uint32_t)t, live);
-        v2bf wb[C][8];   // bf16 pairs: elements (2m, 2m + 1) of the tile
+        // x of the lane's columns: 64 t + 16 q (+ 8 for the second k-block),
+        // or 64 t + 8 q in a half tile
+        const int col = 64 * t + (n < kTile ? 8 : 16) * q;
+        const v8bf x0 = *reinterpret_cast<const v8bf*>(xrow + col);
+        const v8bf x1 = *reinterpret_cast<const v8bf*>(xrow + col + 8);
         #pragma unroll
         for (int c = 0; c < C; c++) {
             uint32_t w[4];
             compose8(ex[c][0], ex[c][1], sm[c][P].x, w[0], w[1]);
             compose8(ex[c][2], ex[c][3], sm[c][P].y, w[2], w[3]);
-            #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (n < kTile) {   // wave-uniform
-                    const int keep = n - 4 * j;
-                    w[j] = keep >= 4 ? w[j] : (keep <= 0 ? 0u : w[j] & ((1u << (8 * keep)) - 1u));
-                }
-                wb[c][2 * j] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[j], 1.0f, false);
-                wb[c][2 * j + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[j], 1.0f, true);
-            }
-        }
-        #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            const v4u* xp = reinterpret_cast<const v4u*>(xs + b * (kGemmMaxSegCols / 2) + t * 8);
-            const v4u x0 = xp[0];
-            const v4u x1 = xp[1];
-            const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            #pragma unroll
-            for (int c = 0; c < C; c++) {
-                float a = acc[c][b];
-                #pragma unroll
-                for (int m = 0; m < 8; m++)
-                    a = __builtin_amdgcn_fdot2_f32_bf16(wb[c][m], __builtin_bit_cast(v2bf, xv[m]),
-                                                        a, false);
-                acc[c][b] = a;
-            }
+            if (n < kTile) { w[2] = 0u; w[3] = 0u; }   // wave-uniform: only n = 8 occurs
+            acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(w[0], w[1]), x0,
+                                                              acc[c], 0, 0, 0);
+            if (n == kTile)
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(w[2], w[3]), x1,
+                                                                  acc[c], 0, 0, 0);
         }
         // sign/mantissa of tile t + kSmAhead (an empty bound past the last tile,
         // as in FusedWave::tile)
@@ -1218,40 +1227,32 @@ struct GemmWave {
 };
 
 // Grid: S * row_blocks workgroups; block (s, rb) decodes row groups
-// [32 rb, 32 rb + 32) of segment s.  R: rows, Rp: rows padded to 64,
-// C: columns, Nc: columns per segment.
-template <int SPS, int NB>
+// [32 rb, 32 rb + 32) of segment s (16 rows each).  R: rows, Rp: rows
+// padded to 64, C: columns, Nc: columns per segment, NB: batch rows.
+template <int SPS>
 __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     const uint32_t* __restrict__ comp, int64_t words, const int64_t* __restrict__ off,
     const uint16_t* __restrict__ st, const v2u* __restrict__ sm, const v2u* __restrict__ table,
-    int64_t Rp, int64_t C, int S, int Nc, int row_blocks, const uint16_t* __restrict__ x,
+    int64_t Rp, int64_t C, int S, int Nc, int row_blocks, const uint16_t* __restrict__ x, int NB,
     float* __restrict__ ws) {
     constexpr uint32_t L = Alpha<SPS>::L;
     constexpr int CH = kGemmChains;
     __shared__ GemmSmem<SPS> smem;
     const int s = (int)(blockIdx.x / (unsigned)row_blocks);
     const int rb = (int)(blockIdx.x % (unsigned)row_blocks);
-    const int64_t n_rg = Rp / kLanes;                       // row groups per segment
+    const int64_t n_rg = Rp / kGemmGroupRows;               // row groups per segment
     // issue the x, table, stream, state and sign/mantissa loads together
     // (as in fused_add_kernel); a wave past the last row group loads the
-    // last one and leaves after the barrier.  x[b][s * Nc + c] is staged at
-    // xs[b][c] (rows of kGemmMaxSegCols), zero past the segment or the
-    // matrix: thread i takes column i % kGemmMaxSegCols of batch rows
-    // i / kGemmMaxSegCols + kXRows * k.
-    constexpr int kXRows = kDecBlock / kGemmMaxSegCols;
-    constexpr int kXPer = kGemmMaxBatch / kXRows;
-    static_assert(kXRows * kGemmMaxSegCols == kDecBlock && kXPer * kXRows == kGemmMaxBatch,
-                  "the x stage is split evenly over the workgroup");
-    const int xc = (int)threadIdx.x % kGemmMaxSegCols;
-    const int xb = (int)threadIdx.x / kGemmMaxSegCols;
+    // last one and leaves after the barrier.  Thread i stages column i of
+    // the segment for every batch row (zero past the segment, the matrix
+    // or the batch).
+    const int xc = (int)threadIdx.x;
     const int64_t xcol = (int64_t)s * Nc + xc;
     const bool x_in = xc < Nc && xcol < C;
-    uint16_t xv[kXPer];
+    uint16_t xv[kGemmMaxBatch];
     #pragma unroll
-    for (int k = 0; k < kXPer; k++) {
-        const int b = xb + kXRows * k;
-        xv[k] = (b < NB && x_in) ? x[(int64_t)b * C + xcol] : (uint16_t)0;
-    }
+    for (int b = 0; b < kGemmMaxBatch; b++)
+        xv[b] = (b < NB && x_in) ? x[(int64_t)b * C + xcol] : (uint16_t)0;
     TableRegs<L> tr;
     table_fetch<L>(tr, table);
     const int lane = threadIdx.x & (kLanes - 1);
@@ -1259,18 +1260,20 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     const int64_t rg0 = (int64_t)rb * kGemmGroupsPerBlock + (int64_t)wave * CH;
     const bool live = rg0 < n_rg;   // wave-uniform
     const int64_t rg_left = n_rg - (int64_t)rb * kGemmGroupsPerBlock;
-    GemmWave<SPS, NB> w;
+    GemmWave<SPS> w;
     w.progress = &smem.dec.progress;
     w.live = (uint32_t)(rg_left >= kGemmGroupsPerBlock ? kDecWaves : (rg_left + CH - 1) / CH);
     w.lane = lane;
+    w.q = lane >> 4;
     w.tbl = smem.dec.tbl;
-    w.xs = smem.xs;
-    w.sm_stride = (int64_t)S * Rp * 8;                      // lanes: S * Rp
-    const int rag = Nc % kTile;
-    w.n_tiles = Nc / kTile + (rag ? 1 : 0);
+    w.xrow = &smem.xs[lane & (kGemmMaxBatch - 1)][0];
+    w.sm_stride = (int64_t)S * n_rg * kLanes * 8;            // lanes: S * n_rg * 64
+    const int per_lane = Nc / 4;                              // elements per lane (8 | per_lane)
+    const int rag = per_lane % kTile;                         // 0 or 8
+    w.n_tiles = per_lane / kTile + (rag ? 1 : 0);
     {
         constexpr int kPairsPerTile = kTile / SPS / 2;
-        const int pairs = (Nc / SPS + 1) / 2;
+        const int pairs = (per_lane / SPS + 1) / 2;
         w.last_pairs = pairs - (w.n_tiles - 1) * kPairsPerTile;
     }
     w.sm_bytes = kLanes * 8u;
@@ -1295,14 +1298,15 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
         }
         const int64_t tn = kSmAhead < w.n_tiles ? kSmAhead : w.n_tiles - 1;
         w.pf[j] = row + tn * w.sm_stride;
-        #pragma unroll
-        for (int b = 0; b < NB; b++) w.acc[j][b] = 0.0f;
+        w.acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    uint16_t* xs16 = reinterpret_cast<uint16_t*>(smem.xs);
     #pragma unroll
-    for (int k = 0; k < kXPer; k++) {
-        const int b = xb + kXRows * k;
-        if (b < NB) xs16[b * kGemmMaxSegCols + xc] = xv[k];
+    for (int b = 0; b < kGemmMaxBatch; b++)
+        smem.xs[b][xc] = __builtin_bit_cast(__bf16, xv[b]);
+    if (xc < kGemmXStride - kGemmMaxSegCols) {
+        #pragma unroll
+        for (int b = 0; b < kGemmMaxBatch; b++)
+            smem.xs[b][kGemmMaxSegCols + xc] = __builtin_bit_cast(__bf16, (uint16_t)0);
     }
     table_store<L>(smem.dec.tbl, tr);
     if (threadIdx.x == 0) smem.dec.progress = 0;
@@ -1314,12 +1318,13 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
         lane_init(w.ch.l[j], w.ch.f[j], lane, kLanes, st0[j], L);
     }
     w.run(rag ? rag : kTile);
+    const int bn = lane & 15;   // the batch row of this lane's sums
+    if (bn >= NB) return;
     #pragma unroll
     for (int j = 0; j < CH; j++) {
         if (rg0 + j >= n_rg) break;
-        const int64_t r = (rg0 + j) * kLanes + lane;
-        #pragma unroll
-        for (int b = 0; b < NB; b++) ws[((int64_t)s * NB + b) * Rp + r] = w.acc[j][b];
+        const int64_t r = (rg0 + j) * kGemmGroupRows + 4 * w.q;
+        *reinterpret_cast<v4f*>(ws + ((int64_t)s * NB + bn) * Rp + r) = w.acc[j];
     }
 }
 
@@ -1370,10 +1375,14 @@ __global__ __launch_bounds__(kFinWaves * kLanes) void gemm_finalize_kernel(
     }
 }
 
-// Uncompressed FP8 skinny GEMM (the baseline of the fused one): a wave
-// takes 4 rows; each lane walks 16-column blocks, converting W to bf16
-// pairs and accumulating v_dot2_f32_bf16 against x read from global memory
-// (cache-resident), then the wave sums its lanes.  C % 16 == 0.
+
+// Uncompressed FP8 GEMV, B = 1 (the baseline of the fused one there): a
+// wave takes 4 rows; each lane walks 16-column blocks, so a wave's load is
+// 1 KiB of one row, converting W to bf16 pairs and accumulating
+// v_dot2_f32_bf16 against x read from global memory (cache-resident), then
+// the wave sums its lanes.  C % 16 == 0.  At one batch row its whole-row
+// loads stream W faster than the matrix-core kernel below (17 against 22 us
+// for 17408 x 5120); from two rows on the matrix-core kernel is faster.
 constexpr int kRawRows = 4;
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -1383,7 +1392,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 template <int NB>
-__global__ __launch_bounds__(256) void gemm_raw_kernel(const v4u* __restrict__ W, int64_t R,
+__global__ __launch_bounds__(256) void gemm_raw_dot2_kernel(const v4u* __restrict__ W, int64_t R,
                                                        int64_t C, const v4u* __restrict__ x,
                                                        float scale, uint16_t* __restrict__ y) {
     const int lane = threadIdx.x & (kLanes - 1);
@@ -1428,6 +1437,64 @@ __global__ __launch_bounds__(256) void gemm_raw_kernel(const v4u* __restrict__ W
             const float v = wave_sum(acc[i][b]);
             if (lane == 0 && r0 + i < R) y[b * R + r0 + i] = bf16_rne(v * scale);
         }
+}
+
+// Uncompressed FP8 skinny GEMM for B >= 2 (the baseline of the fused one
+// there), on the matrix cores as gemm_fused_kernel: a workgroup of nw
+// waves takes 16 rows,
+// and wave w the 64-column blocks w, w + nw, ... of them.  Lane j = 16 q + r
+// loads the 16 bytes of row r at column 64 k + 16 q (two k-blocks of 8, the
+// fused kernel's lane layout) and the matching 32 bytes of x[j % 16] from
+// global memory (cache-resident); the waves' 16 x 16 sums are added in wave
+// order through LDS, so results are deterministic.  C % 16 == 0.
+constexpr int kRawMaxWaves = 16;
+constexpr int kRawUnroll = 4;   // column blocks whose loads a wave issues together
+
+__global__ __launch_bounds__(kRawMaxWaves * kLanes) void gemm_raw_kernel(
+    const v4u* __restrict__ W, int64_t R, int64_t C, const v4u* __restrict__ x, int NB,
+    float scale, uint16_t* __restrict__ y) {
+    __shared__ v4f part[kRawMaxWaves][kLanes];
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int wave = threadIdx.x / kLanes;
+    const int nw = blockDim.x / kLanes;
+    const int q = lane >> 4, r = lane & 15;
+    const int bn = r < NB ? r : 0;                  // x row (lanes r >= NB: sums not stored)
+    const int64_t row0 = (int64_t)blockIdx.x * 16;
+    const int64_t row = row0 + r < R ? row0 + r : R - 1;
+    const int64_t cv = C / 16;                      // 16-byte vectors per W row
+    const v4u* wrow = W + row * cv;
+    const v4u* xrow = x + (int64_t)bn * (C / 8);    // 8 bf16 per 16-byte vector
+    const int64_t blocks = (C + 63) / 64;
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t k0 = wave; k0 < blocks; k0 += (int64_t)nw * kRawUnroll) {
+        v4u wv[kRawUnroll], xa[kRawUnroll], xb[kRawUnroll];
+        #pragma unroll
+        for (int u = 0; u < kRawUnroll; u++) {
+            const int64_t k = k0 + (int64_t)u * nw;
+            const int64_t v = 4 * k + q;            // this lane's 16-byte vector of the row
+            const bool in = k < blocks && v < cv;   // wave-uniform k, per-lane column bound
+            wv[u] = in ? wrow[v] : v4u{0u, 0u, 0u, 0u};
+            xa[u] = in ? xrow[2 * v] : v4u{0u, 0u, 0u, 0u};
+            xb[u] = in ? xrow[2 * v + 1] : v4u{0u, 0u, 0u, 0u};
+        }
+        #pragma unroll
+        for (int u = 0; u < kRawUnroll; u++) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                fp8x8_to_bf16(wv[u].x, wv[u].y), __builtin_bit_cast(v8bf, xa[u]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                fp8x8_to_bf16(wv[u].z, wv[u].w), __builtin_bit_cast(v8bf, xb[u]), acc, 0, 0, 0);
+        }
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0 || r >= NB) return;
+    v4f t = part[0][lane];
+    for (int w = 1; w < nw; w++) t += part[w][lane];
+    #pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int64_t rr = row0 + 4 * q + v;        // lane j holds rows 4 (j / 16) + v
+        if (rr < R) y[(int64_t)r * R + rr] = bf16_rne(t[v] * scale);
+    }
 }
 
 int fail(int code, const std::string& msg) {
@@ -1683,9 +1750,9 @@ int gemm_fused_launch(const void* comp, int64_t comp_bytes, const int64_t* offse
                       void* stream) {
     const int sps = sps_for(log2L);
     if (!sps) return fail(TANS_EINVAL, "gemm_fused: log2L must be 12 (pair) or 11 (nibble)");
-    if (R <= 0 || C <= 0 || S <= 0 || Nc <= 0 || Nc % 2)
-        return fail(TANS_EINVAL, "gemm_fused: need R, C, S > 0 and an even segment width");
-    if (Nc > kGemmMaxSegCols) return fail(TANS_EINVAL, "gemm_fused: segment width above 512");
+    if (R <= 0 || C <= 0 || S <= 0 || Nc <= 0 || Nc % 32)
+        return fail(TANS_EINVAL, "gemm_fused: need R, C, S > 0 and a segment width divisible by 32");
+    if (Nc > kGemmMaxSegCols) return fail(TANS_EINVAL, "gemm_fused: segment width above 1024");
     if (S * Nc < C || (S - 1) * Nc >= C)
         return fail(TANS_EINVAL, "gemm_fused: S segments of Nc columns must cover C exactly");
     if (B < 1 || B > kGemmMaxBatch) return fail(TANS_EINVAL, "gemm_fused: batch must be 1..8");
@@ -1694,31 +1761,24 @@ int gemm_fused_launch(const void* comp, int64_t comp_bytes, const int64_t* offse
     if (comp_bytes < 0 || comp_bytes % 4)
         return fail(TANS_EINVAL, "gemm_fused: compressed size must be a multiple of 4 bytes");
     if (!aligned(comp, 16) || !aligned(sm, 8) || !aligned(offsets, 8) || !aligned(states, 2) ||
-        !aligned(table, 8) || !aligned(x, 2) || !aligned(workspace, 4) || !aligned(y, 2))
-        return fail(TANS_EINVAL, "gemm_fused: misaligned buffer (comp 16, sm 8 bytes)");
+        !aligned(table, 8) || !aligned(x, 2) || !aligned(workspace, 16) || !aligned(y, 2))
+        return fail(TANS_EINVAL, "gemm_fused: misaligned buffer (comp and workspace 16, sm 8 bytes)");
     const int64_t Rp = (R + kLanes - 1) / kLanes * kLanes;
     if (workspace_bytes < S * B * Rp * 4)
         return fail(TANS_EINVAL, "gemm_fused: workspace smaller than S * B * Rp * 4 bytes");
-    const int64_t row_blocks = (Rp / kLanes + kGemmGroupsPerBlock - 1) / kGemmGroupsPerBlock;
+    const int64_t n_rg = Rp / kGemmGroupRows;
+    const int64_t row_blocks = (n_rg + kGemmGroupsPerBlock - 1) / kGemmGroupsPerBlock;
     const int64_t blocks = S * row_blocks;
     if (blocks > INT32_MAX || B * R / 256 + 1 > INT32_MAX)
         return fail(TANS_EINVAL, "gemm_fused: matrix too large");
     hipStream_t st = (hipStream_t)stream;
-#define TANS_GEMM_CASE(S_, NB)                                                                    \
-    case NB:                                                                                      \
-        hipLaunchKernelGGL((gemm_fused_kernel<S_, NB>), dim3((unsigned)blocks), dim3(kDecBlock), 0, \
-                           st, (const uint32_t*)comp, comp_bytes / 4, offsets, states,            \
-                           (const v2u*)sm, (const v2u*)table, Rp, C, (int)S, (int)Nc,             \
-                           (int)row_blocks, (const uint16_t*)x, (float*)workspace);               \
-        break;
-#define TANS_GEMM_SWITCH(S_)                                                                      \
-    switch ((int)B) {                                                                             \
-        TANS_GEMM_CASE(S_, 1) TANS_GEMM_CASE(S_, 2) TANS_GEMM_CASE(S_, 3) TANS_GEMM_CASE(S_, 4)   \
-        TANS_GEMM_CASE(S_, 5) TANS_GEMM_CASE(S_, 6) TANS_GEMM_CASE(S_, 7) TANS_GEMM_CASE(S_, 8)   \
-    }
-    if (sps == 2) { TANS_GEMM_SWITCH(2) } else { TANS_GEMM_SWITCH(1) }
-#undef TANS_GEMM_SWITCH
-#undef TANS_GEMM_CASE
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kDecBlock), 0, st,
+                           (const uint32_t*)comp, comp_bytes / 4, offsets, states, (const v2u*)sm,
+                           (const v2u*)table, Rp, C, (int)S, (int)Nc, (int)row_blocks,
+                           (const uint16_t*)x, (int)B, (float*)workspace);
+    };
+    if (sps == 2) launch(gemm_fused_kernel<2>); else launch(gemm_fused_kernel<1>);
     int rc = hip_check(hipGetLastError(), "gemm_fused_kernel launch");
     if (rc != TANS_OK) return rc;
     hipLaunchKernelGGL(gemm_finalize_kernel, dim3((unsigned)(B * (Rp / kLanes))),
@@ -1738,20 +1798,23 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
     if (!w || !x || !y) return fail(TANS_EINVAL, "gemm_raw: null pointer");
     if (!aligned(w, 16) || !aligned(x, 16) || !aligned(y, 2))
         return fail(TANS_EINVAL, "gemm_raw: W and x must be 16-byte aligned");
-    const int64_t rows_per_block = (256 / kLanes) * kRawRows;
-    const int64_t blocks = (R + rows_per_block - 1) / rows_per_block;
-    if (blocks > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
     hipStream_t st = (hipStream_t)stream;
-#define TANS_RAW_CASE(NB)                                                                         \
-    case NB:                                                                                      \
-        hipLaunchKernelGGL((gemm_raw_kernel<NB>), dim3((unsigned)blocks), dim3(256), 0, st,       \
-                           (const v4u*)w, R, C, (const v4u*)x, scale, (uint16_t*)y);              \
-        break;
-    switch ((int)B) {
-        TANS_RAW_CASE(1) TANS_RAW_CASE(2) TANS_RAW_CASE(3) TANS_RAW_CASE(4)
-        TANS_RAW_CASE(5) TANS_RAW_CASE(6) TANS_RAW_CASE(7) TANS_RAW_CASE(8)
+    if (B == 1) {
+        const int64_t rows_per_block = (256 / kLanes) * kRawRows;
+        const int64_t blocks = (R + rows_per_block - 1) / rows_per_block;
+        if (blocks > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
+        hipLaunchKernelGGL((gemm_raw_dot2_kernel<1>), dim3((unsigned)blocks), dim3(256), 0, st,
+                           (const v4u*)w, R, C, (const v4u*)x, scale, (uint16_t*)y);
+        return hip_check(hipGetLastError(), "gemm_raw_dot2_kernel launch");
     }
-#undef TANS_RAW_CASE
+    const int64_t blocks = (R + 15) / 16;
+    if (blocks > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
+    // waves per workgroup: enough workgroups x waves to fill the GPU about
+    // twice (8192 waves), at most one wave per 64-column block
+    int nw = 1;
+    while (nw < kRawMaxWaves && blocks * nw < 8192 && nw * 64 < C) nw *= 2;
+    hipLaunchKernelGGL(gemm_raw_kernel, dim3((unsigned)blocks), dim3(nw * kLanes), 0, st,
+                       (const v4u*)w, R, C, (const v4u*)x, (int)B, scale, (uint16_t*)y);
     return hip_check(hipGetLastError(), "gemm_raw_kernel launch");
 }
 

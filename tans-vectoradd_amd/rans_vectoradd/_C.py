@@ -283,10 +283,12 @@ def fp8_gemm_fused_tans(m, decode_tbl: torch.Tensor, x: torch.Tensor,
     _check_dev("decode_tbl", decode_tbl, torch.int32)
     x2, B, squeeze = _batch_view(x, C)
     Rp = (R + TANS_LANES - 1) // TANS_LANES * TANS_LANES
-    K = S * Rp
+    K = S * Rp * 4                  # lanes: S segments x Rp / 16 groups x 64
+    _require(Nc % 32 == 0, "segment width must be a multiple of 32")
     _require(m.states.numel() == K, "states do not match the matrix shape")
     _require(m.offsets.numel() == _groups(K) + 1, "offsets do not match the matrix shape")
-    _require(m.sm.numel() == _sm_bytes(K, Nc), "sign/mantissa tiles do not match the matrix shape")
+    _require(m.sm.numel() == _sm_bytes(K, Nc // 4),
+             "sign/mantissa tiles do not match the matrix shape")
     n_states = {"pair": 1 << TANS_PAIR_LOG2L, "nibble": 1 << TANS_NIBBLE_LOG2L}.get(m.alphabet)
     _require(n_states is not None and decode_tbl.numel() == 2 * n_states,
              f"decode_tbl must hold 2 words per state of the matrix's {m.alphabet} alphabet")

@@ -37,7 +37,7 @@ EXPORTS = (
 TANS_LANES = 64
 TANS_TILE = 16
 TANS_GEMM_MAX_BATCH = 8
-TANS_GEMM_MAX_SEG_COLS = 512
+TANS_GEMM_MAX_SEG_COLS = 1024
 TANS_PAIR_LOG2L = 12
 TANS_NIBBLE_LOG2L = 11
 

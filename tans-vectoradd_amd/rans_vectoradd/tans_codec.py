@@ -183,7 +183,10 @@ def compressed_bytes(comp, states, offsets, partial, sm) -> int:
 # Weight matrices for the fused decode-GEMM (no counterpart in the reference)
 # ---------------------------------------------------------------------------
 
-GEMM_BLOCK_ROW_GROUPS = 32    # 64-row groups per workgroup of the GEMM kernel
+GEMM_GROUP_ROWS = 16          # rows of a lane group of the GEMM layout
+GEMM_BLOCK_ROW_GROUPS = 32    # row groups per workgroup of the GEMM kernel
+GEMM_COL_UNIT = 32            # segment widths are multiples of this
+GEMM_MIN_SEG_COLS = 256       # default segments are at least this wide (64 elements per lane)
 GEMM_TARGET_BLOCKS = 256      # workgroups that fill MI355X once (one per CU)
 
 
@@ -218,23 +221,47 @@ class TansMatrix:
 
 
 def gemm_segments(rows: int, cols: int) -> int:
-    """Default column-segment count: enough segments that segments x
-    workgroups-per-segment fills the GPU once, but segments of at least 16
-    and at most 512 columns."""
-    row_groups = -(-rows // TANS_LANES)
-    blocks_per_seg = -(-row_groups // GEMM_BLOCK_ROW_GROUPS)
-    s = min(max(1, GEMM_TARGET_BLOCKS // blocks_per_seg), max(1, cols // 16))
+    """Default column-segment count: the most segments whose workgroups
+    (segments x workgroups per segment) still run in one round, one per CU,
+    so each workgroup's share (and the call's time) is as short as it gets,
+    but segments of at least GEMM_MIN_SEG_COLS columns (shorter lane
+    streams cost more in per-lane state than they save); at least enough
+    segments for the 1024-column limit."""
+    rp = -(-rows // TANS_LANES) * TANS_LANES
+    blocks_per_seg = -(-(rp // GEMM_GROUP_ROWS) // GEMM_BLOCK_ROW_GROUPS)
+    s = min(max(1, GEMM_TARGET_BLOCKS // blocks_per_seg), max(1, cols // GEMM_MIN_SEG_COLS))
     return max(s, -(-cols // TANS_GEMM_MAX_SEG_COLS))
+
+
+def gemm_slab(w: torch.Tensor, S: int, Nc: int) -> torch.Tensor:
+    """The lane streams of a padded matrix w [Rp, S * Nc]: [S * Rp * 4,
+    Nc / 4], lanes ordered (segment, 16-row group, q, r).  Lane (q, r) of a
+    group holds row r of the group and, of each 64-column block of the
+    segment, columns 16 q .. 16 q + 15; of a last block of 32 columns,
+    columns 8 q .. 8 q + 7."""
+    Rp = w.shape[0]
+    G = Rp // GEMM_GROUP_ROWS
+    T, half = divmod(Nc, 64)
+    v = w.reshape(G, GEMM_GROUP_ROWS, S, Nc)
+    full = v[..., :64 * T].reshape(G, GEMM_GROUP_ROWS, S, T, 4, 16)
+    full = full.permute(2, 0, 4, 1, 3, 5).reshape(S, G, 4, GEMM_GROUP_ROWS, 16 * T)
+    parts = [full]
+    if half:
+        tail = v[..., 64 * T:].reshape(G, GEMM_GROUP_ROWS, S, 4, 8)
+        parts.append(tail.permute(2, 0, 3, 1, 4))
+    return torch.cat(parts, dim=-1).reshape(S * G * 4 * GEMM_GROUP_ROWS, Nc // 4).contiguous()
 
 
 def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None,
                   alphabet: str = "pair") -> TansMatrix:
     """tANS-encode an FP8 matrix [R, C] for fp8_gemm_fused_tans.
 
-    Rows are padded to Rp (a multiple of 64) and columns to S * Nc, Nc even
-    and at most 512; segment s holds columns [s Nc, (s + 1) Nc).  The slab
-    view [S * Rp, Nc] (lane s * Rp + r = row r of segment s) is encoded with
-    encode(), so a 64-lane group is 64 rows of one segment.  Padding bytes
+    Rows are padded to Rp (a multiple of 64) and columns to S * Nc, Nc a
+    multiple of 32 and at most 1024; segment s holds columns
+    [s Nc, (s + 1) Nc).  The lane streams gemm_slab() cuts from it are
+    encoded with encode(): a 64-lane group is 16 rows of one segment, each
+    lane holding a quarter of every 64-column block of its row (the A
+    operand of the kernel's 16x16x32 matrix-core products).  Padding bytes
     hold the most frequent exponent (a finite value with a nonzero
     frequency); the kernel multiplies them by zero."""
     if not (isinstance(w_fp8, torch.Tensor) and w_fp8.dim() == 2 and w_fp8.dtype == torch.uint8):
@@ -245,8 +272,7 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
     S = segments if segments is not None else gemm_segments(R, C)
     if S < 1:
         raise ValueError("segments must be >= 1")
-    Nc = -(-C // S)
-    Nc += Nc % 2
+    Nc = -(-C // (S * GEMM_COL_UNIT)) * GEMM_COL_UNIT
     if Nc > TANS_GEMM_MAX_SEG_COLS:
         raise ValueError(f"segments of {Nc} columns exceed {TANS_GEMM_MAX_SEG_COLS}; use more segments")
     S = -(-C // Nc)                       # (S - 1) * Nc < C <= S * Nc
@@ -259,7 +285,7 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
         wp = torch.full((Rp, S * Nc), pad, dtype=torch.uint8)
         wp[:R, :C] = w
         w = wp
-    slab = w.view(Rp, S, Nc).permute(1, 0, 2).reshape(S * Rp, Nc).contiguous()
+    slab = gemm_slab(w, S, Nc)
     comp, states, offsets, partial, sm, freqs, spread = encode(slab, exp_freqs, alphabet=alphabet)
     return TansMatrix(comp, states, offsets, partial, sm, freqs, spread, rows=R, cols=C,
                       segments=S, seg_cols=Nc, alphabet=alphabet)

@@ -94,13 +94,14 @@ def test_gemm_and_gpu_encode_entry_points_validate_before_launch():
     d = P(256)
     f = ctypes.c_float(1.0)
     # gemm_fused(comp, bytes, off, st, sm, tbl, log2L, R, C, S, Nc, x, B, scale, ws, ws_bytes, y, stream)
-    ok = (d, 1024, d, d, d, d, 12, 128, 100, 2, 50, d, 1, f, d, 1 << 20, d, None)
+    ok = (d, 1024, d, d, d, d, 12, 128, 100, 2, 64, d, 1, f, d, 1 << 20, d, None)
     bad = [
         dict(i=6, v=10),            # log2L
         dict(i=12, v=9),            # batch > 8
         dict(i=12, v=0),            # batch < 1
-        dict(i=10, v=51),           # odd segment width
-        dict(i=10, v=600),          # segment width above 512
+        dict(i=10, v=48),           # segment width not a multiple of 32
+        dict(i=10, v=1056),         # segment width above 1024
+        dict(i=14, v=P(260)),       # workspace not 16-byte aligned
         dict(i=9, v=1),             # S * Nc < C
         dict(i=9, v=3),             # (S - 1) * Nc >= C
         dict(i=15, v=16),           # workspace too small

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
+from gemm_layout import gemm_lane_coords
 
 GOLDEN = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_vectors.npz"))
 ALPHABETS = {"pair": (12, 2), "nibble": (11, 1)}
@@ -226,11 +227,12 @@ def test_untile_inverts_the_tiled_layout(T):
 
 @pytest.mark.parametrize("alphabet", list(ALPHABETS))
 @pytest.mark.parametrize("R,C,S", [(17408 // 16, 5120 // 16, None), (100, 70, None), (64, 512, 1),
-                                   (130, 1000, 3), (5, 17, 2)])
+                                   (130, 1000, 3), (5, 17, 2), (70, 96, 1), (64, 2048, None)])
 def test_encode_matrix_slab_layout(T, alphabet, R, C, S):
-    """encode_matrix: rows padded to 64, columns to S * Nc (Nc even, at most
-    512), segment s of row r at lane s * Rp + r; the oracle decodes the
-    encoding back to exactly that padded slab view."""
+    """encode_matrix: rows padded to 64, columns to S * Nc (Nc a multiple of
+    32, at most 1024), lanes in the 16-row group layout; the oracle decodes
+    the encoding back to exactly the padded matrix at each lane's
+    coordinates."""
     from rans_vectoradd import data as D
     q, _ = D.gaussian_fp8_bytes(R * C, seed=R + C)
     w = q.reshape(R, C)
@@ -238,18 +240,35 @@ def test_encode_matrix_slab_layout(T, alphabet, R, C, S):
     m = T.encode_matrix(w, hist, segments=S, alphabet=alphabet)
     Rp = -(-R // 64) * 64
     Nc = m.seg_cols
-    assert Nc % 2 == 0 and Nc <= 512
+    assert Nc % 32 == 0 and Nc <= 1024
     assert (m.segments - 1) * Nc < C <= m.segments * Nc
     if S is not None:
         assert m.segments <= S
     log2L, sps = ALPHABETS[alphabet]
-    K = m.segments * Rp
+    K = m.segments * Rp * 4
     dec = O.w64_decode(m.comp.numpy(), m.offsets.numpy(), m.states.numpy(), m.sm.numpy(),
-                       m.spread.numpy(), m.freqs.numpy(), log2L, sps, K, Nc)
-    slab = dec.reshape(m.segments, Rp, Nc).transpose(1, 0, 2).reshape(Rp, m.segments * Nc)
-    assert np.array_equal(slab[:R, :C], w.numpy())
+                       m.spread.numpy(), m.freqs.numpy(), log2L, sps, K, Nc // 4)
     pad = int(np.argmax(hist.numpy())) << 3
-    assert (slab[R:, :] == pad).all() and (slab[:, C:] == pad).all()
+    full = np.full((Rp, m.segments * Nc), pad, np.uint8)
+    full[:R, :C] = w.numpy()
+    rows, cols = gemm_lane_coords(m.segments, Rp, Nc)
+    assert np.array_equal(dec, full[rows, cols])
+    # every padded-matrix element is held by exactly one lane slot
+    seen = np.zeros(full.shape, np.int64)
+    np.add.at(seen, (rows, cols), 1)
+    assert (seen == 1).all()
+
+
+def test_gemm_segments_fill_one_round():
+    """Config 3/4 shapes: one workgroup per CU at most (<= 256), segment
+    widths multiples of 32."""
+    from rans_vectoradd import tans_codec as T
+    for R, C in ((17408, 5120), (5120, 17408)):
+        S = T.gemm_segments(R, C)
+        Nc = -(-C // (S * 32)) * 32
+        blocks = -(-(R // 16) // 32) * S
+        assert blocks <= 256 and blocks > 200, (R, C, S, blocks)
+        assert (S - 1) * Nc < C <= S * Nc
 
 
 def test_encode_matrix_rejects_bad_input(T):

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+from gemm_layout import matrix_from_lanes
 from oracle import oracle as O
 
 LOG2L = {"pair": (12, 2), "nibble": (11, 1)}
@@ -23,9 +24,9 @@ def _decode_matrix(m):
     log2L, sps = LOG2L[m.alphabet]
     Rp = -(-m.rows // 64) * 64
     dec = O.w64_decode(m.comp.numpy(), m.offsets.numpy(), m.states.numpy(), m.sm.numpy(),
-                       m.spread.numpy(), m.freqs.numpy(), log2L, sps, m.segments * Rp, m.seg_cols)
-    slab = dec.reshape(m.segments, Rp, m.seg_cols).transpose(1, 0, 2).reshape(Rp, -1)
-    return slab[:m.rows, :m.cols]
+                       m.spread.numpy(), m.freqs.numpy(), log2L, sps, m.segments * Rp * 4,
+                       m.seg_cols // 4)
+    return matrix_from_lanes(dec, m.segments, Rp, m.seg_cols, m.rows, m.cols)
 
 
 def test_container_roundtrip(tmp_path):

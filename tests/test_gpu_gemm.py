@@ -120,7 +120,7 @@ def test_gemm_config3_shape_fused_vs_raw(R, B):
 @pytest.mark.parametrize("B", [2, 4, 8])
 @pytest.mark.parametrize("table", ["matched", "laplace"])
 def test_gemm_config4_down_shape(R, B, table):
-    """Config 4's W_down shape (5120 x 17408: 85 segments of 206 columns,
+    """Config 4's W_down shape (5120 x 17408: 25 segments of 704 columns,
     the last one ragged) at the batch sizes the bench times, with the
     matrix's own table and with a mismatched (Laplace) one."""
     from rans_vectoradd import data as D, tans_codec as T
@@ -132,18 +132,20 @@ def test_gemm_config4_down_shape(R, B, table):
     else:
         hist = D.exp_histogram(D.laplace_fp8_bytes(1 << 20, seed=23)[0])
     m = T.encode_matrix(w, hist)
-    assert m.segments == 85 and m.cols % m.seg_cols != 0
+    assert (m.segments, m.seg_cols) == (25, 704) and m.cols % m.seg_cols != 0
     _check(_fused(R, m, x, scale), _reference(w, x, scale))
 
 
 @pytest.mark.parametrize("B", [2, 4])
 def test_gemm_config4_up_shape_batches(R, B):
-    """W_up (17408 x 5120, 28 segments) at the batch sizes between 1 and 8."""
+    """W_up (17408 x 5120: 7 segments of 736 columns, each lane's stream
+    ending in a half tile) at the batch sizes between 1 and 8."""
     from rans_vectoradd import data as D, tans_codec as T
     _say(f"case: gemm 17408x5120 B={B}")
     w, scale = _weights(17408, 5120, seed=31)
     x = _x(B, 5120, seed=32 + B)
     m = T.encode_matrix(w, D.exp_histogram(w))
+    assert (m.segments, m.seg_cols) == (7, 736)
     _check(_fused(R, m, x, scale), _reference(w, x, scale))
 
 

@@ -31,8 +31,8 @@ def _call_noalloc(lib, m, tbl, x, scale):
 def test_noalloc_rejects_products_beyond_its_scratch():
     from rans_vectoradd._lib import lib
     d = ctypes.c_void_p(256)
-    # 100 segments x 8 rows x 17408 outputs of fp32 partial sums: 53 MiB
-    rc = lib.tans_fp8_gemm_fused_noalloc(d, 1024, d, d, d, d, 12, 17408, 5120, 100, 52, d, 8,
+    # 80 segments of 64 columns x 8 rows x 17408 outputs of fp32 partial sums: 42.5 MiB
+    rc = lib.tans_fp8_gemm_fused_noalloc(d, 1024, d, d, d, d, 12, 17408, 5120, 80, 64, d, 8,
                                          ctypes.c_float(1.0), d, None)
     assert rc == -1 and b"16 MiB" in lib.tans_last_error()
 
