@@ -29,7 +29,6 @@ NIBBLE_L = 1 << TANS_NIBBLE_LOG2L
 L = PAIR_L
 M = L
 BLOCK_STREAMS = TANS_LANES   # lanes per group (reference: 128 streams per block)
-TILE_PAIRS = 8               # sign/mantissa tile: 8 pairs = 16 elements
 
 ALPHABETS = {"pair": (256, PAIR_L, 2), "nibble": (16, NIBBLE_L, 1)}
 
@@ -137,24 +136,31 @@ def symbol_freqs(exp_freqs, alphabet: str = "pair") -> np.ndarray:
     return quantize_freqs(p, target=n_states)
 
 
+def _check_tile(tile: int, N: int) -> None:
+    """The reference's condition on encode's tile (tans_codec.py:115-120):
+    0, or a positive tile dividing the N / 2 sign/mantissa pairs."""
+    if not isinstance(tile, (int, np.integer)) or tile < 0 or (tile > 0 and (N // 2) % tile):
+        raise ValueError(f"tile must be 0 or divide N / 2 = {N // 2}; got {tile}")
+
+
 def encode(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair"):
     """tANS-encode FP8 bytes [K, N] (K lanes of N elements, N even).
 
     Returns the reference's 7-tuple: (compressed uint8, states uint16 [K],
     offsets int64 [ceil(K/64)+1], partial uint8 [0], sm uint8 tiles,
-    freqs int32, spread int32).  ``tile`` is accepted for the reference's
-    signature: 0 (standalone decode) and 8 (fused vecadd) give the same
-    16-element sign/mantissa tiles here; other values raise."""
+    freqs int32, spread int32).  ``tile`` is accepted as the reference
+    accepts it (rans_vectoradd/tans_codec.py:115-120: 0, or any tile that
+    divides N / 2; otherwise it raises), but the sign/mantissa layout here
+    is always the 16-element tiles that both decoders read."""
     if not (isinstance(fp8_bytes, torch.Tensor) and fp8_bytes.dim() == 2
             and fp8_bytes.dtype == torch.uint8):
         raise ValueError("fp8_bytes must be a 2-D uint8 tensor [K, N]")
     if alphabet not in ALPHABETS:
         raise ValueError(f"alphabet must be one of {sorted(ALPHABETS)}")
-    if tile not in (0, TILE_PAIRS):
-        raise ValueError(f"tile must be 0 or {TILE_PAIRS}")
     K, N = fp8_bytes.shape
     if N % 2:
         raise ValueError("N must be even")
+    _check_tile(tile, N)
     if isinstance(exp_freqs, torch.Tensor):
         exp_freqs = exp_freqs.detach().cpu().float().numpy()
     freqs = symbol_freqs(exp_freqs, alphabet)
@@ -343,11 +349,10 @@ def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: s
         raise ValueError("encode_gpu needs a GPU tensor; use encode() for CPU tensors")
     if alphabet not in ALPHABETS:
         raise ValueError(f"alphabet must be one of {sorted(ALPHABETS)}")
-    if tile not in (0, TILE_PAIRS):
-        raise ValueError(f"tile must be 0 or {TILE_PAIRS}")
     K, N = fp8_bytes.shape
     if N % 2:
         raise ValueError("N must be even")
+    _check_tile(tile, N)
     if isinstance(exp_freqs, torch.Tensor):
         exp_freqs = exp_freqs.detach().cpu().float().numpy()
     nsym, L, _ = ALPHABETS[alphabet]

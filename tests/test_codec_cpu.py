@@ -206,9 +206,24 @@ def test_encode_argument_checks(T):
     with pytest.raises(ValueError):
         T.encode(torch.zeros((4, 4), dtype=torch.int32), exp)        # dtype
     with pytest.raises(ValueError):
-        T.encode(torch.zeros((4, 4), dtype=torch.uint8), exp, tile=3)
+        T.encode(torch.zeros((4, 4), dtype=torch.uint8), exp, tile=3)     # 3 does not divide 2
+    with pytest.raises(ValueError):
+        T.encode(torch.zeros((4, 4), dtype=torch.uint8), exp, tile=-1)
     with pytest.raises(ValueError):
         T.encode(torch.zeros((4, 4), dtype=torch.uint8), exp, alphabet="triple")
+
+
+def test_encode_accepts_the_references_tiles(T):
+    """Any tile dividing N / 2 is accepted, as by the reference
+    (tans_codec.py:115-120), and gives the same encoding: the sign/mantissa
+    layout is the decoders' 16-element tiles whatever the tile."""
+    from rans_vectoradd import data as D
+    q, _ = D.gaussian_fp8_bytes(70 * 48, seed=3)
+    x = q.reshape(70, 48)
+    ref = T.encode(x, D.exp_histogram(q))
+    for tile in (1, 2, 3, 4, 6, 8, 12, 24):
+        got = T.encode(x, D.exp_histogram(q), tile=tile)
+        assert all(torch.equal(a, b) for a, b in zip(ref, got)), tile
 
 
 def test_empty_input(T):
