@@ -72,6 +72,23 @@ def test_gemm_fused_vs_float64(R, alphabet, rows, cols, B, segments):
     _check(y, _reference(w, x, scale))
 
 
+@pytest.mark.parametrize("alphabet", ["pair", "nibble"])
+@pytest.mark.parametrize("rows,cols,B,segments", [(48, 96, 8, 1), (200, 544, 6, 2),
+                                                  (64, 2048, 2, None), (1, 32, 1, None),
+                                                  (130, 1000, 7, 1)])
+def test_gemm_fused_half_tiles_and_odd_shapes(R, alphabet, rows, cols, B, segments):
+    """Segment widths ending in a half tile (96, 288, 1000 -> 1024 columns of
+    which the last 24 are padding), a single row, one segment of 1024
+    columns, and batches 1-8 on the matrix cores."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: fp8_gemm_fused_tans {rows}x{cols} B={B} S={segments} {alphabet}")
+    w, scale = _weights(rows, cols, seed=rows * 7 + cols)
+    x = _x(B, cols, seed=B + 100)
+    m = T.encode_matrix(w, D.exp_histogram(w), segments=segments, alphabet=alphabet)
+    y = _fused(R, m, x, scale)
+    _check(y, _reference(w, x, scale))
+
+
 def test_gemm_fused_vector_input_and_determinism(R):
     from rans_vectoradd import data as D, tans_codec as T
     _say("case: fp8_gemm_fused_tans vector x, repeated calls")
@@ -87,8 +104,11 @@ def test_gemm_fused_vector_input_and_determinism(R):
 
 
 @pytest.mark.parametrize("rows,cols,B", [(2176, 1280, 1), (2176, 1280, 8), (100, 64, 3),
-                                         (5120, 17408 // 4, 2)])
+                                         (5120, 17408 // 4, 2), (5, 16, 2), (33, 48, 8),
+                                         (17, 80, 5), (40, 1040, 4), (7, 1040, 1)])
 def test_gemm_raw_vs_float64(R, rows, cols, B):
+    """Both raw kernels (row-streaming at B = 1, matrix cores from B = 2),
+    including rows not a multiple of 16 and widths not a multiple of 64."""
     _say(f"case: fp8_gemm_raw {rows}x{cols} B={B}")
     w, scale = _weights(rows, cols, seed=7)
     x = _x(B, cols, seed=8)
