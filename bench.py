@@ -15,7 +15,10 @@ Prints ONE JSON line (progress goes to stderr):
   x_raw         t_raw / t_fused, both the average time per launch of a
                 back-to-back loop (HIP events around single launches add
                 ~5 us to the raw kernel's 130K-workgroup launch, not to the
-                fused kernel's 256)
+                fused kernel's 256).  The headline's raw and fused loops run
+                in alternation, 3 rounds of --steps launches each, so both
+                see the same clocks and board temperature; the median
+                round of each is reported (all rounds under "rounds")
   roofline      compressed HBM bytes of one fused launch / its duration
                 (HIP events around each launch on the launch stream)
   ceiling       what the raw add's launch shape streams with the arithmetic
@@ -190,7 +193,12 @@ def gpu_encode_rate(q_d, hist, lane: int, alphabet: str, reps: int = 5) -> dict:
 
 
 def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps: int,
-                     warmup: int, settle_s: float) -> dict:
+                     warmup: int, settle_s: float, raw_fn=None, rounds: int = 1) -> dict:
+    """One fused configuration.  With raw_fn, the raw kernel and the fused
+    one are timed in alternation for `rounds` rounds of `steps` launches each
+    (raw first), so both see the same clocks and board temperature; the
+    round with the median fused step time is reported, with the median raw
+    round beside it."""
     import torch
     import rans_vectoradd as R
 
@@ -205,10 +213,22 @@ def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps:
     for _ in range(10):
         fn()
     host_us = (time.perf_counter() - t0) / 10 * 1e6      # API call cost on the host
-    kernel_ms, step_ms = timed(fn, steps, warmup, settle_s)
+    extra = {}
+    if raw_fn is None:
+        kernel_ms, step_ms = timed(fn, steps, warmup, settle_s)
+    else:
+        fused_rounds, raw_rounds = [], []
+        for _ in range(rounds):
+            raw_rounds.append(timed(raw_fn, steps, warmup, settle_s))
+            fused_rounds.append(timed(fn, steps, warmup, settle_s))
+        kernel_ms, step_ms = sorted(fused_rounds, key=lambda r: r[1])[rounds // 2]
+        raw_kernel, raw_step = sorted(raw_rounds, key=lambda r: r[1])[rounds // 2]
+        extra = {"raw_kernel_ms": raw_kernel, "raw_step_ms": raw_step,
+                 "rounds_step_ms": [r[1] for r in fused_rounds],
+                 "raw_rounds_step_ms": [r[1] for r in raw_rounds]}
     del args
     torch.cuda.empty_cache()
-    return {"stream_elems": 64 * lane, "lane_elems": lane, "alphabet": alphabet,
+    return extra | {"stream_elems": 64 * lane, "lane_elems": lane, "alphabet": alphabet,
             "kernel_ms": kernel_ms, "step_ms": step_ms, "api_host_us": host_us,
             "bits_per_byte": in_bytes * 8 / (2 * N_ELEMS), "hbm_bytes": hbm_bytes,
             "encode_s": t_enc, "exact_vs_raw": exact,
@@ -635,33 +655,35 @@ def main() -> None:
 
     log("generating inputs")
     qa, qb, hist = make_inputs(args.seed)
-    log("raw and memcpy timing")
     raw_out = R.fp8_vecadd_raw(qa, qb)
-    raw_kernel, raw_step = timed(lambda: R.fp8_vecadd_raw(qa, qb), args.steps, args.warmup,
-                                 args.settle)
-    cpy_kernel, cpy_step = timed(lambda: R.fp8_memcpy(qa), args.steps, args.warmup,
-                                 args.settle)
-    log("streaming ceilings")
-    ceil = run_ceilings(qa, qb, args.steps, args.warmup, args.settle)
-    raw_gbs = 3 * N_ELEMS / (raw_step * 1e-3) / 1e9
-    best21 = max(ceil["stream21_nt"]["gbs"], ceil["stream21_default"]["gbs"])
-    log("  " + "  ".join(f"{k} {v['gbs']:.0f}" for k, v in ceil.items() if isinstance(v, dict))
-        + f" GB/s; raw {raw_gbs:.0f} GB/s = {raw_gbs / best21:.3f} of the 2:1 ceiling")
+    raw_fn = lambda: R.fp8_vecadd_raw(qa, qb)   # noqa: E731
 
     configs = [(HEADLINE_LANE, "pair")]
     if not args.no_sweep:
         configs += [(ln, "pair") for ln in SWEEP_LANES if ln != HEADLINE_LANE]
         configs += [(HEADLINE_LANE, "nibble")]
     results = []
-    for lane, alph in configs:
-        log(f"fused: stream {64 * lane} elements ({lane} per lane), {alph}")
+    raw_kernel = raw_step = None
+    for i, (lane, alph) in enumerate(configs):
+        log(f"fused: stream {64 * lane} elements ({lane} per lane), {alph}"
+            + ("; raw and fused timed in alternation, 3 rounds" if i == 0 else ""))
         r = run_fused_config(qa, qb, raw_out, hist, lane, alph, args.steps, args.warmup,
-                             args.settle)
+                             args.settle, raw_fn=raw_fn if i == 0 else None, rounds=3)
+        if i == 0:
+            raw_kernel, raw_step = r["raw_kernel_ms"], r["raw_step_ms"]
         results.append(r)
         log(f"  kernel {r['kernel_ms'] * 1e3:.1f} us  step {r['step_ms'] * 1e3:.1f} us  "
             f"x_raw {raw_step / r['step_ms']:.3f}  bits/B {r['bits_per_byte']:.3f}  "
             f"exact {r['exact_vs_raw']}  api {r['api_host_us']:.0f} us")
     head = results[0]
+    log("memcpy timing and streaming ceilings")
+    cpy_kernel, cpy_step = timed(lambda: R.fp8_memcpy(qa), args.steps, args.warmup,
+                                 args.settle)
+    ceil = run_ceilings(qa, qb, args.steps, args.warmup, args.settle)
+    raw_gbs = 3 * N_ELEMS / (raw_step * 1e-3) / 1e9
+    best21 = max(ceil["stream21_nt"]["gbs"], ceil["stream21_default"]["gbs"])
+    log("  " + "  ".join(f"{k} {v['gbs']:.0f}" for k, v in ceil.items() if isinstance(v, dict))
+        + f" GB/s; raw {raw_gbs:.0f} GB/s = {raw_gbs / best21:.3f} of the 2:1 ceiling")
     achieved = head["hbm_bytes"] / (head["kernel_ms"] * 1e-3) / 1e9
     line = {
         "metric": "effective GB/s and x raw for fused tANS FP8 vecadd (1 GiB); bits/FP8 byte",
@@ -686,6 +708,8 @@ def main() -> None:
         "exact_vs_raw": head["exact_vs_raw"],
         "kernel_ms": head["kernel_ms"],
         "compressed_hbm_gbs": achieved,
+        "rounds": {"fused_step_ms": head["rounds_step_ms"],
+                   "raw_step_ms": head["raw_rounds_step_ms"]},
         "raw": {"kernel_ms": raw_kernel, "step_ms": raw_step, "gbs": raw_gbs,
                 "frac_of_peak": raw_gbs / HBM_PEAK_GBS,
                 "frac_of_2to1_ceiling": raw_gbs / best21},
