@@ -13,7 +13,9 @@ the metadata key ``tans:name`` with a JSON description:
   for a TansMatrix (the layout of fp8_gemm_fused_tans).
 
 Plain tensors (scales, unencoded weights) are stored under their own names;
-``tans_format`` in the metadata names the layout version.
+``tans_format`` in the metadata names the layout version: v2 streams follow
+the carry-driven refill schedule and matrices the 16-row matrix-core lane
+groups (include/tans_amd.h); files of other versions are refused.
 """
 from __future__ import annotations
 
@@ -23,7 +25,7 @@ import torch
 
 from .tans_codec import TansMatrix, TansTensor
 
-FORMAT = "tans-wave64-v1"
+FORMAT = "tans-wave64-v2"
 _PARTS = ("comp", "states", "offsets", "sm", "freqs", "spread")
 
 
@@ -71,7 +73,8 @@ def load(path: str, device="cpu") -> dict:
     with safe_open(path, framework="pt", device="cpu") as f:
         meta = f.metadata() or {}
         if meta.get("tans_format") != FORMAT:
-            raise ValueError(f"{path}: not a {FORMAT} container")
+            raise ValueError(f"{path}: not a {FORMAT} container (format "
+                             f"{meta.get('tans_format')!r}); re-encode it with this version")
         keys = set(f.keys())
         encoded = {k[len("tans:"):]: json.loads(v) for k, v in meta.items() if k.startswith("tans:")}
         for name, desc in encoded.items():

@@ -76,6 +76,11 @@ def test_container_rejects_other_files(tmp_path):
         container.load(path)
     with pytest.raises(ValueError):
         container.save(path, {"x": torch.zeros(2)}, metadata={"tans_format": "y"})
+    # a file of the previous layout version (other stream schedule and matrix lanes)
+    old = os.path.join(tmp_path, "v1.safetensors")
+    save_file({"x": torch.zeros(2)}, old, metadata={"tans_format": "tans-wave64-v1"})
+    with pytest.raises(ValueError, match="re-encode"):
+        container.load(old)
 
 
 def _checkpoint(path):
