@@ -306,8 +306,8 @@ def gemm_matrix(rows: int, cols: int, seed: int, table_hist=None, alphabet: str 
     q, scale = D.gaussian_fp8_bytes(rows * cols, seed=seed, device="cuda")
     w = q.view(rows, cols)
     hist = D.exp_histogram(q).cpu() if table_hist is None else table_hist
-    m = T.encode_matrix(w.cpu(), hist, alphabet=alphabet)
-    return w, scale, m.to("cuda"), m.decode_table().cuda()
+    m = T.encode_matrix(w, hist, alphabet=alphabet)       # on the GPU (encode_gpu)
+    return w, scale, m, m.decode_table().cuda()
 
 
 def run_gemv_config(seed: int, steps: int, warmup: int, settle_s: float) -> dict:

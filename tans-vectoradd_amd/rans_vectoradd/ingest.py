@@ -104,7 +104,7 @@ def encode_checkpoint(src: str, dst: str, *, alphabet: str = "pair", table: str 
     TansTensor entries of lane_elems elements per lane.  ``table``: "tensor"
     builds each table from the tensor's own histogram, "global" from the
     aggregate of all FP8 tensors.  Non-FP8 tensors are copied unchanged.
-    ``device`` "cuda" encodes lane-layout tensors with the GPU encoder.
+    ``device`` "cuda" encodes with the GPU encoder (matrices and lanes).
     Returns name -> {"kind", "shape", "bits_per_byte"}; the original shape
     and dtype of each encoded entry are kept in the metadata key
     ``shapes``."""
@@ -126,7 +126,7 @@ def encode_checkpoint(src: str, dst: str, *, alphabet: str = "pair", table: str 
             b = t.view(torch.uint8)
             h = glob if glob is not None else hists[name]
             if matrices and b.dim() == 2 and b.shape[1] >= 2:
-                e = encode_matrix(b.contiguous(), h, alphabet=alphabet)
+                e = encode_matrix(b.contiguous().to(device), h, alphabet=alphabet)
                 kind, nbytes = "matrix", e.compressed_bytes()
             else:
                 shp = _lane_shape(b.numel(), lane_elems)

@@ -269,7 +269,9 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
     lane holding a quarter of every 64-column block of its row (the A
     operand of the kernel's 16x16x32 matrix-core products).  Padding bytes
     hold the most frequent exponent (a finite value with a nonzero
-    frequency); the kernel multiplies them by zero."""
+    frequency); the kernel multiplies them by zero.  A GPU tensor is laid
+    out and encoded on its GPU (encode_gpu: the same bytes), and the
+    result's tensors stay there; a CPU tensor is encoded on the CPU."""
     if not (isinstance(w_fp8, torch.Tensor) and w_fp8.dim() == 2 and w_fp8.dtype == torch.uint8):
         raise ValueError("w_fp8 must be a 2-D uint8 tensor [R, C]")
     R, C = w_fp8.shape
@@ -286,13 +288,14 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
     if isinstance(exp_freqs, torch.Tensor):
         exp_freqs = exp_freqs.detach().cpu().double().numpy()
     pad = int(np.argmax(np.asarray(exp_freqs, dtype=np.float64))) << 3
-    w = w_fp8.cpu()
+    w = w_fp8
     if Rp != R or S * Nc != C:
-        wp = torch.full((Rp, S * Nc), pad, dtype=torch.uint8)
+        wp = torch.full((Rp, S * Nc), pad, dtype=torch.uint8, device=w.device)
         wp[:R, :C] = w
         w = wp
     slab = gemm_slab(w, S, Nc)
-    comp, states, offsets, partial, sm, freqs, spread = encode(slab, exp_freqs, alphabet=alphabet)
+    enc = encode_gpu if slab.is_cuda else encode
+    comp, states, offsets, partial, sm, freqs, spread = enc(slab, exp_freqs, alphabet=alphabet)
     return TansMatrix(comp, states, offsets, partial, sm, freqs, spread, rows=R, cols=C,
                       segments=S, seg_cols=Nc, alphabet=alphabet)
 

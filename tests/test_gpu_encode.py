@@ -89,6 +89,25 @@ def test_gpu_encode_edge_cases(R):
         T.encode_gpu(torch.zeros((4, 15), dtype=torch.uint8).cuda(), exp)
 
 
+@pytest.mark.parametrize("alphabet", ["pair", "nibble"])
+@pytest.mark.parametrize("rows,cols,segments", [(17408, 5120, None), (5120, 17408, None),
+                                                (100, 70, None), (130, 1000, 3), (1, 32, None)])
+def test_encode_matrix_on_gpu_equals_cpu(R, alphabet, rows, cols, segments):
+    """encode_matrix of a GPU tensor (padding, lane layout and encoder on the
+    GPU) gives the CPU encoder's bytes, at config 3/4's shapes and ragged
+    ones."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: encode_matrix on GPU {rows}x{cols} S={segments} {alphabet}")
+    q, _ = D.gaussian_fp8_bytes(rows * cols, seed=rows + cols)
+    w = q.reshape(rows, cols)
+    hist = D.exp_histogram(q)
+    a = T.encode_matrix(w.cuda(), hist, segments=segments, alphabet=alphabet)
+    b = T.encode_matrix(w, hist, segments=segments, alphabet=alphabet)
+    assert a.comp.is_cuda and (a.segments, a.seg_cols) == (b.segments, b.seg_cols)
+    for part in ("comp", "states", "offsets", "sm", "freqs", "spread"):
+        assert torch.equal(getattr(a, part).cpu(), getattr(b, part)), part
+
+
 def test_checkpoint_container_on_gpu(R, tmp_path):
     """A checkpoint encoded with the GPU encoder into a container, loaded on
     the GPU: the lane tensor decodes to its bytes and the matrix gives the
