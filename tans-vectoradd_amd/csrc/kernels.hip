@@ -38,14 +38,16 @@
 // words.  The ring holds kSlots segments of 256 words (one 16-byte load per
 // lane) plus a 64-word mirror of its first words, so a wave's 64
 // consecutive reads never wrap.  A stage issues at most one segment load
-// per stream, through a buffer resource whose bound is the room left in
-// the stream, once the segment's ring slot is free.  The loaded segment
-// stays in registers and is written into the ring no earlier than the next
-// stage and no later than the stage in which a lane could first take one of
-// its words.  A stage is four refill checks, so at most 256 words are
-// handed out per stage, and kSlots = kDelay + 2 slots guarantee that a
-// fetched segment starts more than a stage's worth of words ahead of the
-// lanes.
+// per stream, through a buffer resource whose base is the stream's first
+// word and whose bound is the buffer's end, once the segment's ring slot is
+// free.  The loaded segment stays in registers and is written into the
+// ring at the next stage whose slot is free, which comes no later than the
+// stage in which a lane could first take one of its words.  A stage is four
+// refill checks, so at most 256 words are handed out per stage, and
+// kSlots = kDelay + 2 slots guarantee that a fetched segment starts more
+// than a stage's worth of words ahead of the lanes.  Lanes out of range
+// (a tensor's last, partial group) step on a sink table entry that reads
+// no bits, so the refill needs no mask of the lanes in range.
 //
 // FP8 bytes are rebuilt four at a time: the table carries each exponent
 // pre-shifted to bits 6:3 of a byte, a v_perm gathers four of them and one
@@ -300,17 +302,16 @@ constexpr int kDecBlock = kDecWaves * kLanes;
 static_assert((kSlots - 1) * kSegWords >= (kDelay + 1) * kChecksPerStage * kLanes,
               "ring too small for the delay");
 
-// Wave-uniform state of one group's word stream.
+// State of one group's word stream.  Everything but ring_w is wave-uniform.
 struct Feed {
-    const char* next;       // next segment to fetch
-    uint32_t len;           // words in the group's stream (clamped to the buffer)
-    int32_t room;           // bytes from `next` to the end of the buffer (may go below 0)
-    uint32_t next_word;     // stream word index of `next`
-    uint32_t next_slot;     // ring slot of `next`
+    Rsrc src;               // the stream: base at its first word, bound at the buffer's end
+    uint32_t next_b;        // byte offset in the stream of the next segment to fetch
+    uint32_t len_b;         // bytes in the stream (clamped to the buffer)
+    uint32_t next_slot;     // ring slot of the next segment
+    uint32_t dest;          // ring slot of the pending segment
     uint32_t handed;        // words handed to lanes so far
     uint32_t ring_b;        // byte offset in the ring of word `handed`
-    int32_t dest;           // ring slot of the pending (loaded, unwritten) segment, -1 if none
-    uint32_t pend_word;     // stream word index of the pending segment's first word
+    uint32_t ring_w;        // LDS word index of the ring, held in a VGPR (see refill)
     uint32_t* ring;         // this wave's ring for this stream (LDS)
 };
 
@@ -321,88 +322,88 @@ struct Lane {
     uint32_t x8;       // (state - L) * 8: byte offset of the state's table entry
 };
 
-// Segment `next` (the part of it inside the buffer), or nothing.  The bound
-// is the room left in the buffer; a single max keeps it a scalar value (a
-// clamp would become a vector med3, and a non-uniform descriptor makes the
-// compiler loop over its values).
-__device__ __forceinline__ Seg fetch_seg(const Feed& f, bool fetch, int lane) {
-    const int32_t room = f.room > 0 ? f.room : 0;
-    return __builtin_amdgcn_raw_buffer_load_b128(rsrc(f.next, fetch ? (uint32_t)room : 0u),
-                                                 (uint32_t)lane * 16u, 0, 0);
+// A copy of a wave-uniform value in a VGPR (an operand of a VALU
+// instruction that already reads an SGPR must be a VGPR).
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
+    uint32_t v;
+    asm("v_mov_b32 %0, %1" : "=v"(v) : "s"(x));
+    return v;
 }
 
-__device__ __forceinline__ void write_seg(uint32_t* ring, int32_t slot, Seg v, int lane) {
+// Byte offset that reads nothing: every stream bound is below 2^31.
+constexpr uint32_t kNoSeg = 0x80000000u;
+
+// The segment at byte offset b of the stream: the lane's 16 bytes, zeros
+// past the buffer's end.
+__device__ __forceinline__ Seg fetch_seg(const Feed& f, uint32_t b, int lane) {
+    return __builtin_amdgcn_raw_buffer_load_b128(f.src, (uint32_t)lane * 16u + b, 0, 0);
+}
+
+__device__ __forceinline__ void write_seg(uint32_t* ring, uint32_t slot, Seg v, int lane) {
     reinterpret_cast<Seg*>(ring + slot * kSegWords)[lane] = v;
     if (slot == 0 && lane < kMirrorWords / 4)
         reinterpret_cast<Seg*>(ring + kRingWords)[lane] = v;
 }
 
-__device__ __forceinline__ void feed_advance(Feed& f) {
-    f.next += kSegWords * 4;
-    f.room -= kSegWords * 4;
-    f.next_word += kSegWords;
-    f.next_slot = f.next_slot == (uint32_t)(kSlots - 1) ? 0u : f.next_slot + 1;
-}
-
 // Clamp group g's stream to the buffer and fetch its first kSlots segments
-// into `first`; feed_commit writes them to the ring.  The two halves let a
-// kernel issue these loads together with the decode table's, so the stream
-// and the table cost one memory round trip before decoding starts.
+// into `first` (nothing for those past the stream's end); feed_commit
+// writes them to the ring.  The two halves let a kernel issue these loads
+// together with the decode table's, so the stream and the table cost one
+// memory round trip before decoding starts.  lds0 is the start of the
+// workgroup's LDS (the decode table).
 __device__ __forceinline__ void feed_fetch(Feed& f, const uint32_t* comp, int64_t words,
-                                           const int64_t* off, int64_t g, uint32_t* ring, int lane,
-                                           Seg (&first)[kSlots]) {
+                                           const int64_t* off, int64_t g, uint32_t* ring,
+                                           const void* lds0, int lane, Seg (&first)[kSlots]) {
     int64_t s = off[g], e = off[g + 1];
     s = s < 0 ? 0 : (s > words ? words : s);
     e = e < s ? s : (e > words ? words : e);
     const int64_t room = (words - s) * 4;
-    f.next = reinterpret_cast<const char*>(comp + s);
-    f.len = (uint32_t)(e - s);
-    f.room = room > 0x7FFFFFFF ? 0x7FFFFFFF : (int32_t)room;
-    f.next_word = 0;
+    const uint32_t bound = room > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)room;
+    const int64_t len = (e - s) * 4;
+    f.src = rsrc(comp + s, bound);
+    f.len_b = len > (int64_t)bound ? bound : (uint32_t)len;
+    f.next_b = (uint32_t)(kSlots * kSegWords * 4);
     f.next_slot = 0;
-    f.handed = 0;
-    f.ring_b = 0;
     f.ring = ring;
+    f.ring_w = in_vgpr((uint32_t)(reinterpret_cast<const char*>(ring) -
+                                  reinterpret_cast<const char*>(lds0)) / 4u);
     #pragma unroll
     for (int i = 0; i < kSlots; i++) {
-        first[i] = fetch_seg(f, f.next_word < f.len, lane);
-        feed_advance(f);
+        const uint32_t b = (uint32_t)(i * kSegWords * 4);
+        first[i] = fetch_seg(f, b < f.len_b ? b : kNoSeg, lane);
     }
 }
 
+// The last of the first segments becomes the pending one (see feed_stage).
 __device__ __forceinline__ void feed_commit(Feed& f, int lane, const Seg (&first)[kSlots],
                                             Seg& pend) {
     #pragma unroll
     for (int i = 0; i < kSlots; i++) write_seg(f.ring, i, first[i], lane);
-    f.dest = -1;
-    pend = Seg{0u, 0u, 0u, 0u};
-    f.pend_word = 0;
+    pend = first[kSlots - 1];
+    f.dest = kSlots - 1;
 }
 
-// Start of a stage.  The next segment is fetched when it exists and its
-// slot is free (the segment kSlots earlier is consumed).  A loaded segment
-// stays pending in registers until the ring needs it: it is written when
-// the lanes could reach its first word during this stage (they take at
-// most kChecksPerStage * 64 words per stage) or when the next fetch needs
-// its registers.  Writing it only then, not one stage after its load,
-// leaves its load several stages to arrive when the stream is consumed
-// slowly.
+// Start of a stage.  The next segment's slot is free once every word of the
+// segment kSlots earlier in the stream has been handed out.  Then the
+// pending segment (the last one fetched) is written to its slot, and the
+// next segment, when the stream has it, is fetched into the pending
+// registers.  Slots are written only here and from the pending registers,
+// so when nothing was fetched since the pending segment was written, its
+// slot already holds it and writing it again changes nothing.  A fetched
+// segment waits in registers until the next stage whose slot is free: its
+// load has a stage or more to arrive, and the lanes, which take at most
+// kChecksPerStage * 64 words per stage, reach its first word no earlier
+// than the stage after that one.
 __device__ __forceinline__ void feed_stage(Feed& f, Seg& pend, int lane) {
     static_assert(kDelay == 1, "one pending segment per stream");
-    const int32_t d = f.dest;
-    const uint32_t free_to = f.handed + (uint32_t)((kSlots - 1) * kSegWords) + 1;
-    const uint32_t lim = f.len < free_to ? f.len : free_to;
-    const bool fetch = f.next_word < lim;
-    const bool due = f.pend_word < f.handed + (uint32_t)(kChecksPerStage * kLanes);
-    if (d >= 0 && (fetch || due)) {
-        write_seg(f.ring, d, pend, lane);
-        f.dest = -1;
-    }
-    if (fetch) {
-        pend = fetch_seg(f, true, lane);
-        f.dest = (int32_t)f.next_slot;
-        f.pend_word = f.next_word;
-        feed_advance(f);
+    if (f.next_b <= 4u * f.handed + (uint32_t)((kSlots - 1) * kSegWords * 4)) {   // wave-uniform
+        write_seg(f.ring, f.dest, pend, lane);
+        if (f.next_b < f.len_b) {
+            pend = fetch_seg(f, f.next_b, lane);
+            f.dest = f.next_slot;
+            f.next_b += (uint32_t)(kSegWords * 4);
+            f.next_slot = f.next_slot == (uint32_t)(kSlots - 1) ? 0u : f.next_slot + 1;
+        }
     }
 }
 
@@ -444,61 +445,74 @@ __device__ __forceinline__ Mask dec_pair(Lane& l, const v2u* __restrict__ tbl, u
     return add_carry(l.q, e1.x + e2.x);
 }
 
+// (c << 2) + b in one SALU instruction (s_lshl2_add_u32, which sets SCC).
+__device__ __forceinline__ uint32_t lshl2_add(uint32_t c, uint32_t b) {
+    uint32_t d;
+    asm("s_lshl2_add_u32 %0, %1, %2" : "=s"(d) : "s"(c), "s"(b) : "scc");
+    return d;
+}
+
 // Lanes in `need` take the next words of the stream in lane order (mbcnt
 // rank, one ds_read_b32 from the ring); lanes in `shift` (a superset) move
 // hi into lo.  Every lane reads the ring (in bounds: the mirror covers the
-// 64 words past the ring end), so there is no divergent branch.
-__device__ __forceinline__ void refill(Lane& l, Feed& f, Mask shift, Mask need) {
-    const uint32_t rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(need >> 32),
-                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)need, 0u));
+// 64 words past the ring end), so there is no divergent branch.  The mbcnt
+// accumulator adds the ring's word index to the rank, so the read address
+// is one shift-add of the rank and the wave's ring offset.  lds0 is the
+// start of the workgroup's LDS.
+__device__ __forceinline__ void refill(Lane& l, Feed& f, const void* lds0, Mask shift,
+                                       Mask need) {
+    const uint32_t idx = __builtin_amdgcn_mbcnt_hi((uint32_t)(need >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)need,
+                                                                             f.ring_w));
     const uint32_t w = *reinterpret_cast<const uint32_t*>(
-        reinterpret_cast<const char*>(f.ring) + f.ring_b + rank * 4u);
+        reinterpret_cast<const char*>(lds0) + f.ring_b + idx * 4u);
     l.lo = select(shift, l.hi, l.lo);
     l.hi = select(need, w, l.hi);
     const uint32_t c = (uint32_t)__popcll(need);
     f.handed += c;
-    const uint32_t nb = f.ring_b + c * 4u;
+    const uint32_t nb = lshl2_add(c, f.ring_b);
     const uint32_t wrapped = nb - (uint32_t)(kRingWords * 4);
     f.ring_b = nb < wrapped ? nb : wrapped;   // (nb mod ring size), as an unsigned min
 }
 
-// The refill check after a step pair (`carry` from dec_pair, `active` the
-// lanes in range).  A lane whose low window word is used up (at most 32
-// unread bits) shifts and takes the next word.  After the second-to-last
-// step pair of the stream (final_check) it still shifts but takes a word
-// only below 24 unread bits (pos > 8 after the shift), since the last pair
-// reads at most 24.  There is no check after the last pair.
-__device__ __forceinline__ void check(Lane& l, Feed& f, Mask carry, Mask active,
+// The refill check after a step pair (`carry` from dec_pair; lanes out of
+// range never carry, see lane_init).  A lane whose low window word is used
+// up (at most 32 unread bits) shifts and takes the next word.  After the
+// second-to-last step pair of the stream (final_check) it still shifts but
+// takes a word only below 24 unread bits (pos > 8 after the shift), since
+// the last pair reads at most 24.  There is no check after the last pair.
+__device__ __forceinline__ void check(Lane& l, Feed& f, const void* lds0, Mask carry,
                                       bool final_check) {
-    const Mask shift = carry & active;
     if (final_check) {
-        refill(l, f, shift, shift & __ballot((l.q & 31u) > 8u));
+        refill(l, f, lds0, carry, carry & __ballot((l.q & 31u) > 8u));
     } else {
-        refill(l, f, shift, shift);
+        refill(l, f, lds0, carry, carry);
     }
 }
 
 // check() in the last tile, with its kind chosen at run time (wave-uniform
 // flags selecting lane masks): none after the stream's last step pair, the
 // final check after the second-to-last one.
-__device__ __forceinline__ void check_last(Lane& l, Feed& f, Mask carry, Mask active,
+__device__ __forceinline__ void check_last(Lane& l, Feed& f, const void* lds0, Mask carry,
                                            bool final_check, bool none) {
     const Mask below24 = __ballot((l.q & 31u) > 8u);
-    const Mask shift = none ? Mask(0) : carry & active;
-    refill(l, f, shift, final_check ? shift & below24 : shift);
+    const Mask shift = none ? Mask(0) : carry;
+    refill(l, f, lds0, shift, final_check ? shift & below24 : shift);
 }
 
-// Start a chain (after feed_commit): every active lane takes two words, the
-// first `lanes` stream words being the lanes' first words and the next
-// `lanes` their second; pos = 0.
+// Start a chain (after feed_commit): every lane in range takes two words,
+// the first `lanes` stream words being the lanes' first words and the next
+// `lanes` their second; pos = 0.  A lane out of range starts on the sink
+// entry (byte offset `sink` from the table), whose steps read no bits and
+// return to it, so its pos never moves and its refill checks never fire.
 __device__ __forceinline__ void lane_init(Lane& l, Feed& f, int lane, int lanes, uint16_t state,
-                                          uint32_t L) {
+                                          uint32_t L, uint32_t sink) {
     const bool active = lane < lanes;
     const uint32_t* r = f.ring;
     l.lo = active ? r[lane] : 0u;
     l.hi = active ? r[lanes + lane] : 0u;
     l.q = 0;
-    l.x8 = ((uint32_t)(state - L) & (L - 1)) * 8u;
+    l.x8 = active ? ((uint32_t)(state - L) & (L - 1)) * 8u : sink;
     f.handed = 2u * (uint32_t)lanes;
     f.ring_b = 8u * (uint32_t)lanes;
 }
@@ -570,6 +584,19 @@ struct DecSmem {
     v2u tbl[Alpha<SPS>::L];
     uint32_t rings[kDecWaves][C][kRingAlloc];
     uint32_t progress;   // tiles finished by all waves of the workgroup
+    v2u sink;            // the table entry of lanes out of range (lane_init)
+
+    // The sink's byte offset from the table.
+    __device__ __forceinline__ uint32_t sink_off() const {
+        return (uint32_t)(reinterpret_cast<const char*>(&sink) -
+                          reinterpret_cast<const char*>(tbl));
+    }
+    // By one thread before the workgroup's first barrier.  The sink reads
+    // no bits (word0 = 0: nb = 0, exponents 0) and leads back to itself.
+    __device__ __forceinline__ void init() {
+        progress = 0;
+        sink = v2u{0u, sink_off()};
+    }
 };
 
 // Keep the waves of a workgroup abreast.  The SIMD arbiter prefers older
@@ -611,7 +638,7 @@ struct Chains {
 // table, and its bytes are discarded).
 template <int SPS, int C, bool LAST>
 __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ tbl, int lane,
-                                         uint32_t (&ex)[C][4], const Mask (&act)[C],
+                                         uint32_t (&ex)[C][4],
                                          int last_pairs = 4 * Alpha<SPS>::kStagesPerTile) {
     #pragma unroll
     for (int c = 0; c < C; c++) ch.l[c].q &= 0xF800001Fu;
@@ -633,11 +660,11 @@ __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ 
                 const int idx = h * kChecksPerStage + q;
                 #pragma unroll
                 for (int c = 0; c < C; c++)
-                    check_last(ch.l[c], ch.f[c], carry[c], act[c], idx == last_pairs - 2,
+                    check_last(ch.l[c], ch.f[c], tbl, carry[c], idx == last_pairs - 2,
                                idx >= last_pairs - 1);
             } else {
                 #pragma unroll
-                for (int c = 0; c < C; c++) check(ch.l[c], ch.f[c], carry[c], act[c], false);
+                for (int c = 0; c < C; c++) check(ch.l[c], ch.f[c], tbl, carry[c], false);
             }
         }
         #pragma unroll
@@ -677,13 +704,12 @@ struct FusedWave {
     int n_tiles;
     int lane;
     int base;               // tiles this wave finished in earlier groups (pacing)
-    Mask act[C];            // lanes in range, per chain
 
     // Tile t, with P = t mod kSmAhead; LAST: t is the last tile.
     template <int P, bool LAST>
     __device__ __forceinline__ void tile(int t) {
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, act);
+        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex);
         pace(progress, lane, (uint32_t)(base + t), live);
         #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -747,7 +773,6 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     w.out_stride = K * 16;
     Seg first[C][kSlots];
     uint16_t st0[C];
-    bool act[C];
     int glanes[G];
     // the loads of the groups gbase .. gbase + G - 1
     auto setup = [&](int64_t gbase) {
@@ -761,13 +786,12 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
             w.sm_bytes[j] = (uint32_t)lanes * 8u;
             w.out_cur[j] = reinterpret_cast<char*>(out + k0);
-            feed_fetch(w.ch.f[2 * j], a_comp, a_words, a_off, g, smem.rings[wave][2 * j], lane,
-                       first[2 * j]);
+            feed_fetch(w.ch.f[2 * j], a_comp, a_words, a_off, g, smem.rings[wave][2 * j], tbl,
+                       lane, first[2 * j]);
             feed_fetch(w.ch.f[2 * j + 1], b_comp, b_words, b_off, g, smem.rings[wave][2 * j + 1],
-                       lane, first[2 * j + 1]);
+                       tbl, lane, first[2 * j + 1]);
             st0[2 * j] = a_st[k0 + lane_ld];
             st0[2 * j + 1] = b_st[k0 + lane_ld];
-            act[2 * j] = act[2 * j + 1] = active;
             glanes[j] = lanes;
             const char* rows[2] = {reinterpret_cast<const char*>(a_sm + k0),
                                    reinterpret_cast<const char*>(b_sm + k0)};
@@ -788,7 +812,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     };
     setup(g0);
     table_store<L>(tbl, tr);
-    if (threadIdx.x == 0) smem.progress = 0;
+    if (threadIdx.x == 0) smem.init();
     __syncthreads();
     if (!live) return;
     int done = 0;   // tiles of earlier groups (the pacing count runs on)
@@ -796,8 +820,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
         #pragma unroll
         for (int c = 0; c < C; c++) {
             feed_commit(w.ch.f[c], lane, first[c], w.ch.p[c]);
-            lane_init(w.ch.l[c], w.ch.f[c], lane, glanes[c / 2], st0[c], L);
-            w.act[c] = __ballot(act[c]);
+            lane_init(w.ch.l[c], w.ch.f[c], lane, glanes[c / 2], st0[c], L, smem.sink_off());
         }
         w.base = done;
         // the first n_tiles - 1 tiles four per iteration, then the last one,
@@ -897,7 +920,6 @@ struct DecodeWave {
     int base;               // tiles this wave finished in earlier groups (pacing)
     bool full;              // both groups have 64 lanes in range (wave-uniform)
     bool lines;             // K % 16 == 0: rows start 16-byte aligned
-    Mask act[C];            // lanes in range, per group
     int last_pairs;         // step pairs of the streams in the last tile
 
     // Tile t (P = t mod kSmAhead) holding n elements per lane (n < 16 only
@@ -908,7 +930,7 @@ struct DecodeWave {
         // symbol come after every real one (no refill checks there), stay
         // inside the table, and their bytes are not stored.
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, act, last_pairs);
+        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, last_pairs);
         pace(progress, lane, (uint32_t)(base + t), live);
         uint32_t w[C][4];
         #pragma unroll
@@ -1044,7 +1066,6 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     w.lines = K % 16 == 0;
     Seg first[C][kSlots];
     uint16_t st0[C];
-    bool act[C];
     // the loads of the groups gbase, gbase + 1
     auto setup = [&](int64_t gbase) {
         bool full = true;
@@ -1060,9 +1081,8 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
             const bool active = lane < lanes;
             const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
             w.sm_bytes[j] = (uint32_t)lanes * 8u;
-            feed_fetch(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], lane, first[j]);
+            feed_fetch(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], tbl, lane, first[j]);
             st0[j] = st[k0 + lane_ld];
-            act[j] = active;
             const char* row = reinterpret_cast<const char*>(sm + k0);
             #pragma unroll
             for (int i = 0; i < kSmAhead; i++) {
@@ -1078,7 +1098,7 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     };
     setup(g0);
     table_store<L>(tbl, tr);
-    if (threadIdx.x == 0) smem.progress = 0;
+    if (threadIdx.x == 0) smem.init();
     __syncthreads();
     if (!live) return;
     int done = 0;   // tiles of earlier groups (the pacing count runs on)
@@ -1086,8 +1106,7 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
         #pragma unroll
         for (int j = 0; j < C; j++) {
             feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
-            lane_init(w.ch.l[j], w.ch.f[j], lane, w.lanes[j], st0[j], L);
-            w.act[j] = __ballot(act[j]);
+            lane_init(w.ch.l[j], w.ch.f[j], lane, w.lanes[j], st0[j], L, smem.sink_off());
         }
         w.base = done;
         w.run(rag ? rag : kTile);
@@ -1174,8 +1193,7 @@ struct GemmWave {
         // and its bytes past n are zeroed; every lane of a group is in range
         // (rows are padded to 64)
         uint32_t ex[C][4];
-        const Mask all[C] = {~Mask(0), ~Mask(0)};
-        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, all, last_pairs);
+        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, last_pairs);
         pace(progress, lane, (uint32_t)t, live);
         // x of the lane's columns: 64 t + 16 q (+ 8 for the second k-block),
         // or 64 t + 8 q in a half tile
@@ -1286,7 +1304,8 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
         const int64_t rg = rg0 + j < n_rg ? rg0 + j : n_rg - 1;
         const int64_t g = (int64_t)s * n_rg + rg;
         const int64_t k0 = g * kLanes;
-        feed_fetch(w.ch.f[j], comp, words, off, g, smem.dec.rings[wave][j], lane, first[j]);
+        feed_fetch(w.ch.f[j], comp, words, off, g, smem.dec.rings[wave][j], smem.dec.tbl, lane,
+                   first[j]);
         st0[j] = st[k0 + lane];
         const char* row = reinterpret_cast<const char*>(sm + k0);
         #pragma unroll
@@ -1309,13 +1328,13 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
             smem.xs[b][kGemmMaxSegCols + xc] = __builtin_bit_cast(__bf16, (uint16_t)0);
     }
     table_store<L>(smem.dec.tbl, tr);
-    if (threadIdx.x == 0) smem.dec.progress = 0;
+    if (threadIdx.x == 0) smem.dec.init();
     __syncthreads();
     if (!live) return;
     #pragma unroll
     for (int j = 0; j < CH; j++) {
         feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
-        lane_init(w.ch.l[j], w.ch.f[j], lane, kLanes, st0[j], L);
+        lane_init(w.ch.l[j], w.ch.f[j], lane, kLanes, st0[j], L, smem.dec.sink_off());
     }
     w.run(rag ? rag : kTile);
     const int bn = lane & 15;   // the batch row of this lane's sums
