@@ -28,6 +28,11 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
+# The decoders' one atomic is a single lane's LDS add per tile (the pacing
+# count).  The atomic optimizer rewrites it for a whole wave (mbcnt, a
+# compare and a second exec mask: 6 VALU and 6 SALU per tile), so it is off
+# for kernels.hip.
+KERNEL_FLAGS = ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
 CXX_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-fopenmp", "-Wall", "-Wextra"]
 
 
@@ -49,10 +54,11 @@ def build(asm: bool = False) -> str:
     kern_o = os.path.join(BUILD, "kernels.o")
     enc_o = os.path.join(BUILD, "encode.o")
     _run(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, "codec.cpp"), "-o", codec_o])
-    _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "kernels.hip"), "-o", kern_o])
+    _run([HIPCC, *HIP_FLAGS, *KERNEL_FLAGS, "-c", os.path.join(CSRC, "kernels.hip"),
+          "-o", kern_o])
     _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, "encode.hip"), "-o", enc_o])
     if asm:
-        _run([HIPCC, *HIP_FLAGS, "--cuda-device-only", "-S",
+        _run([HIPCC, *HIP_FLAGS, *KERNEL_FLAGS, "--cuda-device-only", "-S",
               os.path.join(CSRC, "kernels.hip"), "-o", os.path.join(BUILD, "kernels.s")])
     tmp = OUT + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, codec_o, kern_o, enc_o,

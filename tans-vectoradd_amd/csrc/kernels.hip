@@ -612,13 +612,9 @@ __device__ __forceinline__ void pace(uint32_t* progress, int lane, uint32_t done
                                                    __HIP_MEMORY_SCOPE_WORKGROUP);
     before = __builtin_amdgcn_readfirstlane(before);
     const uint32_t mine = done * live;   // compare done with before / live
-    if (mine > before + 2 * live) {
-        __builtin_amdgcn_s_setprio(0);
-    } else if (mine + live <= before) {
-        __builtin_amdgcn_s_setprio(3);
-    } else {
-        __builtin_amdgcn_s_setprio(1);
-    }
+    __builtin_amdgcn_s_setprio(1);
+    if (mine > before + 2 * live) __builtin_amdgcn_s_setprio(0);
+    if (mine + live <= before) __builtin_amdgcn_s_setprio(3);
 }
 
 // C independent chains (a chain = one group's stream) decoded in lockstep
