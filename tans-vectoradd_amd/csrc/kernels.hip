@@ -345,16 +345,17 @@ __device__ __forceinline__ void write_seg(uint32_t* ring, uint32_t slot, Seg v, 
         reinterpret_cast<Seg*>(ring + kRingWords)[lane] = v;
 }
 
-// Clamp group g's stream to the buffer and fetch its first kSlots segments
-// into `first` (nothing for those past the stream's end); feed_commit
-// writes them to the ring.  The two halves let a kernel issue these loads
-// together with the decode table's, so the stream and the table cost one
-// memory round trip before decoding starts.  lds0 is the start of the
-// workgroup's LDS (the decode table).
+// Clamp a group's stream (words s .. e of comp) to the buffer and fetch its
+// first kSlots segments into `first` (nothing for those past the stream's
+// end); feed_commit writes them to the ring.  The two halves let a kernel
+// issue these loads together with the decode table's, so the stream and the
+// table cost one memory round trip before decoding starts.  Callers read the
+// stream offsets of all their chains before the first call, so those scalar
+// loads share one round trip too.  lds0 is the start of the workgroup's LDS
+// (the decode table).
 __device__ __forceinline__ void feed_fetch(Feed& f, const uint32_t* comp, int64_t words,
-                                           const int64_t* off, int64_t g, uint32_t* ring,
+                                           int64_t s, int64_t e, uint32_t* ring,
                                            const void* lds0, int lane, Seg (&first)[kSlots]) {
-    int64_t s = off[g], e = off[g + 1];
     s = s < 0 ? 0 : (s > words ? words : s);
     e = e < s ? s : (e > words ? words : e);
     const int64_t room = (words - s) * 4;
@@ -782,9 +783,10 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
             w.sm_bytes[j] = (uint32_t)lanes * 8u;
             w.out_cur[j] = reinterpret_cast<char*>(out + k0);
-            feed_fetch(w.ch.f[2 * j], a_comp, a_words, a_off, g, smem.rings[wave][2 * j], tbl,
+            const int64_t sa = a_off[g], ea = a_off[g + 1], sb = b_off[g], eb = b_off[g + 1];
+            feed_fetch(w.ch.f[2 * j], a_comp, a_words, sa, ea, smem.rings[wave][2 * j], tbl,
                        lane, first[2 * j]);
-            feed_fetch(w.ch.f[2 * j + 1], b_comp, b_words, b_off, g, smem.rings[wave][2 * j + 1],
+            feed_fetch(w.ch.f[2 * j + 1], b_comp, b_words, sb, eb, smem.rings[wave][2 * j + 1],
                        tbl, lane, first[2 * j + 1]);
             st0[2 * j] = a_st[k0 + lane_ld];
             st0[2 * j + 1] = b_st[k0 + lane_ld];
@@ -1066,9 +1068,16 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     auto setup = [&](int64_t gbase) {
         bool full = true;
         w.out_tile = out + gbase * kLanes;
+        // a wave past the last group repeats it with no lanes in range
+        int64_t os[C], oe[C];
         #pragma unroll
         for (int j = 0; j < C; j++) {
-            // a wave past the last group repeats it with no lanes in range
+            const int64_t g = gbase + j < n_groups ? gbase + j : n_groups - 1;
+            os[j] = off[g];
+            oe[j] = off[g + 1];
+        }
+        #pragma unroll
+        for (int j = 0; j < C; j++) {
             const int64_t g = gbase + j < n_groups ? gbase + j : n_groups - 1;
             const int64_t k0 = g * kLanes;
             const int lanes = gbase + j < n_groups ? (K - k0 < kLanes ? (int)(K - k0) : kLanes) : 0;
@@ -1077,7 +1086,8 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
             const bool active = lane < lanes;
             const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
             w.sm_bytes[j] = (uint32_t)lanes * 8u;
-            feed_fetch(w.ch.f[j], comp, words, off, g, smem.rings[wave][j], tbl, lane, first[j]);
+            feed_fetch(w.ch.f[j], comp, words, os[j], oe[j], smem.rings[wave][j], tbl, lane,
+                       first[j]);
             st0[j] = st[k0 + lane_ld];
             const char* row = reinterpret_cast<const char*>(sm + k0);
             #pragma unroll
@@ -1293,15 +1303,22 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     w.sm_bytes = kLanes * 8u;
     Seg first[CH][kSlots];
     uint16_t st0[CH];
+    // a wave with one row group left repeats it as its second chain and
+    // discards that chain's sums
+    int64_t os[CH], oe[CH];
     #pragma unroll
     for (int j = 0; j < CH; j++) {
-        // a wave with one row group left repeats it as its second chain and
-        // discards that chain's sums
+        const int64_t g = (int64_t)s * n_rg + (rg0 + j < n_rg ? rg0 + j : n_rg - 1);
+        os[j] = off[g];
+        oe[j] = off[g + 1];
+    }
+    #pragma unroll
+    for (int j = 0; j < CH; j++) {
         const int64_t rg = rg0 + j < n_rg ? rg0 + j : n_rg - 1;
         const int64_t g = (int64_t)s * n_rg + rg;
         const int64_t k0 = g * kLanes;
-        feed_fetch(w.ch.f[j], comp, words, off, g, smem.dec.rings[wave][j], smem.dec.tbl, lane,
-                   first[j]);
+        feed_fetch(w.ch.f[j], comp, words, os[j], oe[j], smem.dec.rings[wave][j], smem.dec.tbl,
+                   lane, first[j]);
         st0[j] = st[k0 + lane];
         const char* row = reinterpret_cast<const char*>(sm + k0);
         #pragma unroll
