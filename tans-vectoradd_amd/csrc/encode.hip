@@ -8,16 +8,17 @@
 //
 // Passes (all on the caller's stream):
 //   enc_backward_kernel  one thread per lane: step chunks [S][K] (u16:
-//                        value in bits 11:0, nb in bits 15:12) and the
-//                        initial decoder state
-//   enc_pack_kernel      one wave per group: each lane packs its chunks into
-//                        words [w][K]; the wave replays the refill schedule
-//                        to count the group's stream words (padded to 4)
-//                        and records at which checks each lane takes a word
+//                        value in bits 11:0, nb in bits 15:12), the
+//                        initial decoder state, and the number of stream
+//                        words the lane takes (a closed form of the refill
+//                        schedule in the lane's bit counts), summed per
+//                        group (padded to 4)
 //   enc_scan_kernel      exclusive prefix of the group counts -> offsets
-//   enc_interleave_kernel one wave per group: replays the schedule from those
-//                        bits and writes each taken word at offset + handed
-//                        + rank
+//   enc_place_kernel     one wave per group: replays the schedule while
+//                        each lane packs its chunks into words; a word's
+//                        place (offset + handed + rank) is fixed when the
+//                        lane takes it, and the word is stored there when
+//                        its last bit is packed
 //   enc_sm_kernel        sign/mantissa tiles
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -59,24 +60,17 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-// Workspace layout: chunks u16 [S][K], words u32 [max_words][K],
-// nwords u32 [K], glen u32 [G], takes u32 [ceil(pairs / 32)][K] (bit q % 32
-// of word q / 32: the lane takes a word after step pair q).
+// Workspace layout: chunks u16 [S][K], glen u32 [G].
 struct WsLayout {
-    int64_t chunks, words, nwords, glen, takes, total;
+    int64_t chunks, glen, total;
 };
 
-WsLayout ws_layout(int64_t K, int64_t S, int32_t log2L) {
+WsLayout ws_layout(int64_t K, int64_t S) {
     const int64_t G = (K + kLanes - 1) / kLanes;
-    const int64_t max_words = (S * log2L + 31) / 32 + 1;
-    const int64_t take_words = ((S + 1) / 2 + 31) / 32;
     WsLayout l;
     l.chunks = 0;
-    l.words = align256(S * K * 2);
-    l.nwords = l.words + align256(max_words * K * 4);
-    l.glen = l.nwords + align256(K * 4);
-    l.takes = l.glen + align256(G * 4);
-    l.total = l.takes + align256(take_words * K * 4);
+    l.glen = align256(S * K * 2);
+    l.total = l.glen + align256(G * 4);
     return l;
 }
 
@@ -129,12 +123,13 @@ __device__ __forceinline__ uint2 enc_consts(uint32_t e, int log2L) {
 // row (a scalar base; the lane's offset k * 2 is fixed), so the store costs
 // no per-step address arithmetic.
 __device__ __forceinline__ void enc_step(uint32_t s, const uint2* tab, const uint16_t* nx,
-                                         uint32_t L, uint32_t& x, uint32_t& bad,
+                                         uint32_t L, uint32_t& x, uint32_t& bad, uint32_t& bits,
                                          uint16_t* __restrict__ chunks, int64_t i, int64_t K,
                                          uint32_t koff) {
     const uint2 e = tab[s];
     bad |= e.x;
     const uint32_t nb = __builtin_amdgcn_ubfe(x + e.x, 16u, 5u);
+    bits += nb;
     const uint32_t ch = __builtin_amdgcn_ubfe(x, 0u, nb) | (nb << 12);
     __builtin_amdgcn_raw_buffer_store_b16((uint16_t)ch,
                                           __builtin_amdgcn_make_buffer_rsrc(chunks + i * K, (short)0,
@@ -147,6 +142,8 @@ __device__ __forceinline__ void enc_step(uint32_t s, const uint2* tab, const uin
 }
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef uint64_t Mask;   // a lane mask of the wave
 constexpr int kEncBlockChunks = 8;   // 16-byte chunks per 128-byte block of a row
 
 // Symbol of step q of a 16-byte chunk: bytes 2q, 2q + 1 (pair) or byte q.
@@ -171,17 +168,44 @@ __device__ __forceinline__ void load_block(v4u (&b)[kEncBlockChunks], const v4u*
     }
 }
 
+// The refill schedule: every lane in range starts with two words (64 bits);
+// steps 2q and 2q + 1 consume their nb bits, and after that step pair, if it
+// is not the last, a lane holding at most 32 bits takes the next word (+32
+// bits); after the second-to-last pair only a lane holding fewer than 24
+// does.  A pair consumes at most 24 bits, so after every check but the final
+// one a lane holds 33..64 bits: with c the bits consumed so far it has taken
+// floor(c / 32) + 2 words.  The words a lane takes in all are therefore
+// fixed by its bit count up to the third-to-last pair (c3) and up to the
+// second-to-last (c2): t = floor(c3 / 32) + 2, plus one when 32 t - c2 < 24
+// (t = 2, c3 = 0 with two pairs; 2 words with one pair; none for S = 0).
+// The walk records its bit count after the last pair (b1: bits of steps
+// 2 (n - 1) ..) and after the second-to-last (b2: steps 2 (n - 2) ..), so
+// c2 = bits - b1 and c3 = bits - b2.
+__device__ __forceinline__ uint32_t lane_words(int64_t S, uint32_t bits, uint32_t b1,
+                                               uint32_t b2) {
+    if (S == 0) return 0u;
+    const int64_t n = (S + 1) / 2;   // step pairs
+    if (n == 1) return 2u;
+    const uint32_t c2 = bits - b1;
+    const uint32_t c3 = n >= 3 ? bits - b2 : 0u;
+    const uint32_t t = c3 / 32u + 2u;
+    return t + (32u * t - c2 < (uint32_t)kRefillFinalBelow ? 1u : 0u);
+}
+
 // One thread per lane walks its row backwards.  When rows are 16-byte
 // aligned (N % 16 == 0) a lane loads its row 128 bytes at a time and the
 // next 128 bytes while it encodes the current ones: a step then waits on
 // LDS only, not on a global load, and each line of the row is fetched in
 // one go (the lanes' rows are N bytes apart, so a line read piecewise over
-// many steps could leave the cache in between).
+// many steps could leave the cache in between).  A wave is one 64-lane
+// group (blocks hold four); its lanes' word counts are summed into
+// glen[group], padded to a multiple of 4.
 template <int SPS>
 __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     const uint8_t* __restrict__ fp8, int64_t K, int64_t N, const uint32_t* __restrict__ enc_tab,
     const uint16_t* __restrict__ next, int log2L, uint16_t* __restrict__ chunks,
-    uint16_t* __restrict__ states, int* __restrict__ status) {
+    uint16_t* __restrict__ states, uint32_t* __restrict__ glen, int* __restrict__ status) {
+    static_assert(kEncBlock % kLanes == 0, "blocks hold whole groups");
     constexpr int NSYM = SPS == 2 ? 256 : 16;
     __shared__ uint2 tab[NSYM];
     __shared__ uint16_t nx[1 << TANS_PAIR_LOG2L];
@@ -190,123 +214,60 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     for (uint32_t i = threadIdx.x; i < L; i += blockDim.x) nx[i] = next[i];
     __syncthreads();
     const int64_t k = (int64_t)blockIdx.x * kEncBlock + threadIdx.x;
-    if (k >= K) return;
+    if (k - (threadIdx.x & (kLanes - 1)) >= K) return;   // the whole group is out of range
     const int64_t S = N / SPS;
-    const int64_t row = k * N;
-    uint32_t x = L;
-    uint32_t bad = 0;   // bit 31: a symbol of frequency 0
-    const uint32_t koff = (uint32_t)k * 2u;   // K <= INT32_MAX (checked by the launcher)
-    if (N % 16 == 0) {   // kernel-uniform
-        constexpr int kQ = 16 / SPS;   // steps per chunk
-        const v4u* rp = reinterpret_cast<const v4u*>(fp8 + row);
-        const int64_t nch = N / 16;
-        v4u cur[kEncBlockChunks], nxt[kEncBlockChunks];
-        load_block(cur, rp, nch);
-        for (int64_t hi = nch; hi > 0; hi -= kEncBlockChunks) {
-            load_block(nxt, rp, hi - kEncBlockChunks);
-            #pragma unroll
-            for (int c = 0; c < kEncBlockChunks; c++) {
-                const int64_t j = hi - 1 - c;
-                if (j < 0) break;   // wave-uniform
-                static_for<0, kQ>([&](auto Q) {
-                    constexpr int q = kQ - 1 - decltype(Q)::value;
-                    enc_step(chunk_symbol<SPS, q>(cur[c]), tab, nx, L, x, bad, chunks,
-                             j * kQ + q, K, koff);
-                });
-            }
-            #pragma unroll
-            for (int c = 0; c < kEncBlockChunks; c++) cur[c] = nxt[c];
-        }
-    } else {
-        for (int64_t i = S - 1; i >= 0; i--)
-            enc_step(symbol_at<SPS>(fp8, row + i * SPS, K * N), tab, nx, L, x, bad, chunks, i, K,
-                     koff);
-    }
-    states[k] = (uint16_t)x;
-    if (bad >> 31) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
-}
-
-// The refill schedule: every active lane starts with two words (64 bits);
-// steps 2q and 2q + 1 consume their nb bits, and after that step pair, if
-// it is not the last, a lane holding at most 32 bits takes the next word
-// (+32 bits); after the second-to-last pair only a lane holding fewer than
-// 24 does.  This pass replays it while it packs each lane's chunks into
-// words, and records per pair whether the lane takes a word, so
-// enc_interleave_kernel needs only those bits.  Chunks are read 16 steps at
-// a time (a step past S reads as an empty chunk).
-constexpr int kPackChecks = 8;
-
-__global__ __launch_bounds__(kEncBlock) void enc_pack_kernel(
-    const uint16_t* __restrict__ chunks, int64_t K, int64_t S, int64_t max_words,
-    uint32_t* __restrict__ words, uint32_t* __restrict__ nwords, uint32_t* __restrict__ glen,
-    uint32_t* __restrict__ takes) {
-    const int lane = threadIdx.x & (kLanes - 1);
-    const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) + threadIdx.x / kLanes;
-    const int64_t G = (K + kLanes - 1) / kLanes;
-    if (g >= G) return;   // wave-uniform
-    const int64_t k = g * kLanes + lane;
-    const bool active = k < K;
-    const int64_t kk = active ? k : K - 1;
-    uint64_t acc = 0;
-    int n = 0;
-    uint32_t nw = 0, taken = 0, tw = 0;
-    int cnt = 0;
-    if (S > 0) {
-        taken = 2;
-        cnt = 64;
-    }
-    const int64_t n_pairs = (S + 1) / 2;
-    static_assert(32 % kPackChecks == 0, "a batch of pairs never straddles a takes word");
-    for (int64_t q0 = 0; q0 < n_pairs; q0 += kPackChecks) {
-        uint32_t c[2 * kPackChecks];
-        #pragma unroll
-        for (int u = 0; u < 2 * kPackChecks; u++) {
-            const int64_t t = 2 * q0 + u;
-            c[u] = t < S ? chunks[t * K + kk] : 0u;   // wave-uniform condition
-        }
-        #pragma unroll
-        for (int u = 0; u < kPackChecks; u++) {
-            const int64_t q = q0 + u;
-            if (q >= n_pairs) break;   // wave-uniform
-            #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint32_t ch = c[2 * u + h];
-                const int nb = (int)(ch >> 12);
-                cnt -= nb;
-                acc |= (uint64_t)(ch & 0xFFFu) << n;
-                n += nb;
-                if (n >= 32) {
-                    if (active && nw < max_words) words[(int64_t)nw * K + k] = (uint32_t)acc;
-                    nw++;
-                    acc >>= 32;
-                    n -= 32;
+    uint32_t words = 0;
+    if (k < K) {
+        const int64_t row = k * N;
+        uint32_t x = L;
+        uint32_t bad = 0;    // bit 31: a symbol of frequency 0
+        uint32_t bits = 0;          // the lane's stream bits
+        uint32_t b1 = 0, b2 = 0;    // bits of the last pair, of the last two (lane_words)
+        const uint32_t koff = (uint32_t)k * 2u;   // K <= INT32_MAX (checked by the launcher)
+        if (N % 16 == 0) {   // kernel-uniform
+            // S is a multiple of 8, so the last two pairs are the first four
+            // steps of the walk, all in the row's last chunk
+            constexpr int kQ = 16 / SPS;   // steps per chunk
+            const v4u* rp = reinterpret_cast<const v4u*>(fp8 + row);
+            const int64_t nch = N / 16;
+            v4u cur[kEncBlockChunks], nxt[kEncBlockChunks];
+            load_block(cur, rp, nch);
+            for (int64_t hi = nch; hi > 0; hi -= kEncBlockChunks) {
+                load_block(nxt, rp, hi - kEncBlockChunks);
+                #pragma unroll
+                for (int c = 0; c < kEncBlockChunks; c++) {
+                    const int64_t j = hi - 1 - c;
+                    if (j < 0) break;   // wave-uniform
+                    static_for<0, kQ>([&](auto Q) {
+                        constexpr int q = kQ - 1 - decltype(Q)::value;
+                        enc_step(chunk_symbol<SPS, q>(cur[c]), tab, nx, L, x, bad, bits, chunks,
+                                 j * kQ + q, K, koff);
+                        if constexpr (q == kQ - 2) {
+                            if (j == nch - 1) b1 = bits;   // wave-uniform
+                        } else if constexpr (q == kQ - 4) {
+                            if (j == nch - 1) b2 = bits;
+                        }
+                    });
                 }
+                #pragma unroll
+                for (int c = 0; c < kEncBlockChunks; c++) cur[c] = nxt[c];
             }
-            if (q + 1 < n_pairs) {   // wave-uniform: no check after the last pair
-                const int below = q + 2 == n_pairs ? kRefillFinalBelow : kRefillAtMost + 1;
-                if (cnt < below) {
-                    taken++;
-                    cnt += 32;
-                    tw |= 1u << (q % 32);
-                }
+        } else {
+            const int64_t last = 2 * ((S + 1) / 2 - 1);   // first step of the last pair
+            for (int64_t i = S - 1; i >= 0; i--) {
+                enc_step(symbol_at<SPS>(fp8, row + i * SPS, K * N), tab, nx, L, x, bad, bits,
+                         chunks, i, K, koff);
+                if (i == last) b1 = bits;
+                if (i == last - 2) b2 = bits;
             }
         }
-        const int64_t qe = q0 + kPackChecks;
-        if (qe % 32 == 0 || qe >= n_pairs) {   // wave-uniform
-            if (active) takes[(q0 / 32) * K + k] = tw;
-            tw = 0;
-        }
+        states[k] = (uint16_t)x;
+        if (bad >> 31) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
+        words = lane_words(S, bits, b1, b2);
     }
-    if (n > 0) {
-        if (active && nw < max_words) words[(int64_t)nw * K + k] = (uint32_t)acc;
-        nw++;
-    }
-    if (active) nwords[k] = nw;
-    // group total: the words active lanes take, padded to a multiple of 4
-    uint32_t tot = active ? taken : 0u;
     #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m, kLanes);
-    if (lane == 0) glen[g] = (tot + 3u) & ~3u;
+    for (int m = 32; m >= 1; m >>= 1) words += __shfl_xor(words, m, kLanes);
+    if ((threadIdx.x & (kLanes - 1)) == 0) glen[k / kLanes] = (words + 3u) & ~3u;
 }
 
 // offsets[g] = sum of glen[0..g), offsets[G] = total; one workgroup: each
@@ -342,14 +303,21 @@ __global__ __launch_bounds__(kEncBlock) void zero_words_kernel(uint32_t* __restr
     if (i < n) p[i] = 0u;
 }
 
-// Replays the schedule from the take bits of enc_pack_kernel: first the two
-// initial words of every active lane (the first words in lane order, then
-// the second), then after each step pair the lanes taking a word write it
-// at offset + handed + rank (ballot + mbcnt, the order the decoders read),
-// 32 pairs per take word with the word loads of 8 pairs issued together.
-__global__ __launch_bounds__(kEncBlock) void enc_interleave_kernel(
-    const uint32_t* __restrict__ takes, int64_t K, int64_t S, int64_t max_words,
-    const uint32_t* __restrict__ words, const uint32_t* __restrict__ nwords,
+// One wave per group replays the refill schedule while each lane packs its
+// chunks into 32-bit words, LSB first.  A word's place in the stream is
+// fixed when the lane takes it: the first two words of every lane are the
+// first 2 x lanes words (first words in lane order, then the second), and
+// a word taken after a step pair goes to handed + rank (ballot + mbcnt,
+// the order the decoders read it).  A word is stored when its last bit is
+// packed, which comes after it is taken (a pair adds at most 24 bits, and
+// a lane takes a word only once it holds at most 32), so each lane keeps
+// the places of at most two taken, unfinished words.  Words taken past the
+// lane's bits, and the group's padding to 4 words, are zero.  The stores go
+// through a buffer resource bounded by the group's length.
+constexpr int kPlaceBatch = 8;   // step pairs whose chunks are loaded together
+
+__global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
+    const uint16_t* __restrict__ chunks, int64_t K, int64_t S,
     const int64_t* __restrict__ offsets, uint32_t* __restrict__ comp) {
     const int lane = threadIdx.x & (kLanes - 1);
     const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) + threadIdx.x / kLanes;
@@ -357,56 +325,69 @@ __global__ __launch_bounds__(kEncBlock) void enc_interleave_kernel(
     if (g >= G) return;   // wave-uniform
     const int64_t k = g * kLanes + lane;
     const bool active = k < K;
-    const uint32_t nw = active ? nwords[k] : 0u;
+    const int64_t kk = active ? k : K - 1;
+    const uint32_t lanes = (uint32_t)(K - g * kLanes < kLanes ? K - g * kLanes : kLanes);
     const int64_t base = offsets[g];
-    const int64_t end = offsets[g + 1];
-    int64_t handed = 0;
-    uint32_t taken = 0;
-    if (S > 0) {
-        const int64_t lanes = K - g * kLanes < kLanes ? K - g * kLanes : kLanes;
+    const int64_t glen = offsets[g + 1] - base;
+    const Rsrc out = __builtin_amdgcn_make_buffer_rsrc(
+        comp + base, (short)0, (int)(glen > 0x1FFFFFFF ? 0x7FFFFFFF : glen * 4), 0x00020000);
+    const int64_t n_pairs = (S + 1) / 2;
+    uint64_t acc = 0;   // packed bits not yet stored
+    uint32_t n = 0;     // how many
+    uint32_t f0 = (uint32_t)lane, f1 = lanes + (uint32_t)lane;   // places of unfinished words
+    uint32_t fc = S > 0 && active ? 2u : 0u;                      // how many
+    int32_t held = 64;  // bits the lane holds
+    uint32_t handed = S > 0 ? 2u * lanes : 0u;
+    for (int64_t q0 = 0; q0 < n_pairs; q0 += kPlaceBatch) {
+        uint32_t c[2 * kPlaceBatch];
         #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int64_t pos = base + r * lanes + lane;
-            if (active && pos < end)
-                comp[pos] = (uint32_t)r < nw && r < max_words ? words[(int64_t)r * K + k] : 0u;
+        for (int u = 0; u < 2 * kPlaceBatch; u++) {
+            const int64_t t = 2 * q0 + u;
+            c[u] = t < S ? chunks[t * K + kk] : 0u;   // wave-uniform condition
         }
-        handed = 2 * lanes;
-        taken = 2;
-    }
-    const int64_t n_checks = (S + 1) / 2 - 1;   // a check after every step pair but the last
-    constexpr int kBatch = 8;
-    for (int64_t q0 = 0; q0 < n_checks; q0 += 32) {
-        const uint32_t tw = active ? takes[(q0 / 32) * K + k] : 0u;
-        for (int b = 0; b < 32; b += kBatch) {
-            if (q0 + b >= n_checks) break;   // wave-uniform
-            uint32_t w[kBatch];
-            #pragma unroll
-            for (int u = 0; u < kBatch; u++) {   // this lane's words of the batch
-                const uint32_t t = taken + (uint32_t)__builtin_popcount(tw & ((1u << (b + u)) - 1u) &
-                                                                        ~((1u << b) - 1u));
-                const bool take = (tw >> (b + u)) & 1u;
-                w[u] = (take && t < nw && t < max_words) ? words[(int64_t)t * K + k] : 0u;
+        #pragma unroll
+        for (int u = 0; u < kPlaceBatch; u++) {
+            const int64_t q = q0 + u;
+            if (q >= n_pairs) break;   // wave-uniform
+            const uint32_t nb0 = c[2 * u] >> 12, nb1 = c[2 * u + 1] >> 12;
+            acc |= (uint64_t)((c[2 * u] & 0xFFFu) | ((c[2 * u + 1] & 0xFFFu) << nb0)) << n;
+            n += nb0 + nb1;
+            held -= (int32_t)(nb0 + nb1);
+            if (n >= 32) {   // at most one word per pair (n < 32 + 24)
+                if (active)
+                    __builtin_amdgcn_raw_buffer_store_b32((uint32_t)acc, out, f0 * 4u, 0, 0);
+                f0 = f1;
+                fc--;
+                acc >>= 32;
+                n -= 32;
             }
-            #pragma unroll
-            for (int u = 0; u < kBatch; u++) {
-                if (q0 + b + u >= n_checks) break;   // wave-uniform
-                const bool need = (tw >> (b + u)) & 1u;
-                const uint64_t m = __ballot(need);
+            if (q + 1 < n_pairs) {   // wave-uniform: no check after the last pair
+                const int32_t below = q + 2 == n_pairs ? kRefillFinalBelow : kRefillAtMost + 1;
+                const bool need = active && held < below;
+                const Mask m = __ballot(need);
                 const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
                     (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
                 if (need) {
-                    const int64_t pos = base + handed + rank;
-                    if (pos < end) comp[pos] = w[u];
+                    if (fc == 0) f0 = handed + rank; else f1 = handed + rank;
+                    fc++;
+                    held += 32;
                 }
-                handed += __popcll(m);
+                handed += (uint32_t)__popcll(m);
             }
-            taken += (uint32_t)__builtin_popcount(tw & (((b + kBatch) >= 32 ? 0xFFFFFFFFu
-                                                                          : ((1u << (b + kBatch)) - 1u)) &
-                                                        ~((1u << b) - 1u)));
         }
     }
-    // zero padding up to the 4-word boundary
-    if (base + handed + lane < end) comp[base + handed + lane] = 0u;
+    if (active) {
+        if (n > 0) {   // the last, partial word
+            __builtin_amdgcn_raw_buffer_store_b32((uint32_t)acc, out, f0 * 4u, 0, 0);
+            f0 = f1;
+            fc--;
+        }
+        if (fc >= 1) __builtin_amdgcn_raw_buffer_store_b32(0u, out, f0 * 4u, 0, 0);
+        if (fc >= 2) __builtin_amdgcn_raw_buffer_store_b32(0u, out, f1 * 4u, 0, 0);
+    }
+    // padding up to the 4-word boundary
+    if ((int64_t)handed + lane < glen)
+        __builtin_amdgcn_raw_buffer_store_b32(0u, out, (handed + (uint32_t)lane) * 4u, 0, 0);
 }
 
 // Sign/mantissa tiles: sm[(t K + k) * 8] from bytes [16t, 16t + 16) of row
@@ -485,7 +466,7 @@ int tans_gpu_encode_workspace(int64_t K, int64_t N, int32_t log2L, int64_t* work
     if (log2L != TANS_PAIR_LOG2L && log2L != TANS_NIBBLE_LOG2L)
         return fail(TANS_EINVAL, "gpu_encode: log2L must be 12 (pair) or 11 (nibble)");
     const int64_t S = log2L == TANS_PAIR_LOG2L ? N / 2 : N;
-    *workspace_bytes = ws_layout(K, S, log2L).total;
+    *workspace_bytes = ws_layout(K, S).total;
     return TANS_OK;
 }
 
@@ -512,31 +493,24 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
     const int sps = log2L == TANS_PAIR_LOG2L ? 2 : 1;
     const int64_t S = N / sps;
     const int64_t G = (K + kLanes - 1) / kLanes;
-    const int64_t max_words = (S * log2L + 31) / 32 + 1;
     const int64_t n_tiles = (N + kTile - 1) / kTile;
     if (K > INT32_MAX || S > (int64_t(1) << 24) || n_tiles * K / kEncBlock + 1 > INT32_MAX)
         return fail(TANS_EINVAL, "gpu_encode: tensor too large");
-    const WsLayout l = ws_layout(K, S, log2L);
+    const WsLayout l = ws_layout(K, S);
     char* ws = static_cast<char*>(workspace);
     uint16_t* chunks = reinterpret_cast<uint16_t*>(ws + l.chunks);
-    uint32_t* words = reinterpret_cast<uint32_t*>(ws + l.words);
-    uint32_t* nwords = reinterpret_cast<uint32_t*>(ws + l.nwords);
     uint32_t* glen = reinterpret_cast<uint32_t*>(ws + l.glen);
     hipStream_t st = (hipStream_t)stream;
     const unsigned lane_blocks = (unsigned)((K + kEncBlock - 1) / kEncBlock);
-    const unsigned group_blocks = (unsigned)((G + kEncBlock / kLanes - 1) / (kEncBlock / kLanes));
     if (sps == 2)
         hipLaunchKernelGGL(enc_backward_kernel<2>, dim3(lane_blocks), dim3(kEncBlock), 0, st,
                            (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
-                           states, status);
+                           states, glen, status);
     else
         hipLaunchKernelGGL(enc_backward_kernel<1>, dim3(lane_blocks), dim3(kEncBlock), 0, st,
                            (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
-                           states, status);
+                           states, glen, status);
     if ((rc = hip_check(hipGetLastError(), "enc_backward_kernel launch"))) return rc;
-    hipLaunchKernelGGL(enc_pack_kernel, dim3(group_blocks), dim3(kEncBlock), 0, st, chunks, K, S,
-                       max_words, words, nwords, glen, reinterpret_cast<uint32_t*>(ws + l.takes));
-    if ((rc = hip_check(hipGetLastError(), "enc_pack_kernel launch"))) return rc;
     hipLaunchKernelGGL(enc_scan_kernel, dim3(1), dim3(1024), 0, st, glen, G, offsets);
     if ((rc = hip_check(hipGetLastError(), "enc_scan_kernel launch"))) return rc;
     const int64_t sm_blocks = (K + kSmRows - 1) / kSmRows * ((n_tiles + kSmCols - 1) / kSmCols);
@@ -560,15 +534,13 @@ int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* work
         const int sps = log2L == TANS_PAIR_LOG2L ? 2 : 1;
         const int64_t S = N / sps;
         const int64_t G = (K + kLanes - 1) / kLanes;
-        const int64_t max_words = (S * log2L + 31) / 32 + 1;
-        const WsLayout l = ws_layout(K, S, log2L);
+        const WsLayout l = ws_layout(K, S);
         const char* ws = static_cast<const char*>(workspace);
-        hipLaunchKernelGGL(enc_interleave_kernel,
+        hipLaunchKernelGGL(enc_place_kernel,
                            dim3((unsigned)((G + kEncBlock / kLanes - 1) / (kEncBlock / kLanes))),
-                           dim3(kEncBlock), 0, st, reinterpret_cast<const uint32_t*>(ws + l.takes),
-                           K, S, max_words, reinterpret_cast<const uint32_t*>(ws + l.words),
-                           reinterpret_cast<const uint32_t*>(ws + l.nwords), offsets, c32);
-        if ((rc = hip_check(hipGetLastError(), "enc_interleave_kernel launch"))) return rc;
+                           dim3(kEncBlock), 0, st, reinterpret_cast<const uint16_t*>(ws + l.chunks),
+                           K, S, offsets, c32);
+        if ((rc = hip_check(hipGetLastError(), "enc_place_kernel launch"))) return rc;
     }
     hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((kTailWords + kEncBlock - 1) / kEncBlock)),
                        dim3(kEncBlock), 0, st, c32 + words_total, kTailWords);
