@@ -12,14 +12,15 @@
 //                        initial decoder state, and the number of stream
 //                        words the lane takes (a closed form of the refill
 //                        schedule in the lane's bit counts), summed per
-//                        group (padded to 4)
+//                        group (padded to 4); for rows of whole 16-byte
+//                        tiles also the sign/mantissa tiles
 //   enc_scan_kernel      exclusive prefix of the group counts -> offsets
 //   enc_place_kernel     one wave per group: replays the schedule while
 //                        each lane packs its chunks into words; a word's
 //                        place (offset + handed + rank) is fixed when the
 //                        lane takes it, and the word is stored there when
 //                        its last bit is packed
-//   enc_sm_kernel        sign/mantissa tiles
+//   enc_sm_kernel        sign/mantissa tiles when rows are not whole tiles
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -158,6 +159,15 @@ __device__ __forceinline__ uint32_t chunk_symbol(const v4u& c) {
     }
 }
 
+// The two sign/mantissa words of a 16-byte tile: sign and mantissa bits
+// (mask 0x87 of each byte) of bytes 0-3 in place and of bytes 4-7 rotated
+// by 4 bits into the exponent positions, the same for bytes 8-15.
+__device__ __forceinline__ void sm_words(const uint32_t (&b)[4], uint32_t& w0, uint32_t& w1) {
+    const uint32_t m = 0x87878787u;
+    w0 = (b[0] & m) | __builtin_amdgcn_alignbit(b[1] & m, b[1] & m, 28u);
+    w1 = (b[2] & m) | __builtin_amdgcn_alignbit(b[3] & m, b[3] & m, 28u);
+}
+
 // Chunks top - 1, top - 2, ... of a row into b[0], b[1], ... (zero below 0).
 __device__ __forceinline__ void load_block(v4u (&b)[kEncBlockChunks], const v4u* rp,
                                            int64_t top) {
@@ -204,7 +214,8 @@ template <int SPS>
 __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     const uint8_t* __restrict__ fp8, int64_t K, int64_t N, const uint32_t* __restrict__ enc_tab,
     const uint16_t* __restrict__ next, int log2L, uint16_t* __restrict__ chunks,
-    uint16_t* __restrict__ states, uint32_t* __restrict__ glen, int* __restrict__ status) {
+    uint16_t* __restrict__ states, uint32_t* __restrict__ glen, uint32_t* __restrict__ sm,
+    int* __restrict__ status) {
     static_assert(kEncBlock % kLanes == 0, "blocks hold whole groups");
     constexpr int NSYM = SPS == 2 ? 256 : 16;
     __shared__ uint2 tab[NSYM];
@@ -248,6 +259,12 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
                             if (j == nch - 1) b2 = bits;
                         }
                     });
+                    // the chunk is tile j: its sign/mantissa words (a wave's
+                    // stores cover 512 contiguous bytes)
+                    const uint32_t tb[4] = {cur[c].x, cur[c].y, cur[c].z, cur[c].w};
+                    uint32_t w0, w1;
+                    sm_words(tb, w0, w1);
+                    *reinterpret_cast<uint2*>(sm + (j * K + k) * 2) = uint2{w0, w1};
                 }
                 #pragma unroll
                 for (int c = 0; c < kEncBlockChunks; c++) cur[c] = nxt[c];
@@ -400,12 +417,6 @@ constexpr int kSmRows = 32;                      // rows per workgroup
 constexpr int kSmCols = kLanes;                  // tiles per workgroup
 constexpr int kSmPad = kSmRows + 1;              // LDS row stride (records): 2-way banks at most
 
-__device__ __forceinline__ void sm_words(const uint32_t (&b)[4], uint32_t& w0, uint32_t& w1) {
-    const uint32_t m = 0x87878787u;
-    w0 = (b[0] & m) | __builtin_amdgcn_alignbit(b[1] & m, b[1] & m, 28u);
-    w1 = (b[2] & m) | __builtin_amdgcn_alignbit(b[3] & m, b[3] & m, 28u);
-}
-
 __global__ __launch_bounds__(kEncBlock) void enc_sm_kernel(const uint8_t* __restrict__ fp8,
                                                            int64_t K, int64_t N, int64_t n_tiles,
                                                            uint32_t* __restrict__ sm) {
@@ -505,14 +516,15 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
     if (sps == 2)
         hipLaunchKernelGGL(enc_backward_kernel<2>, dim3(lane_blocks), dim3(kEncBlock), 0, st,
                            (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
-                           states, glen, status);
+                           states, glen, (uint32_t*)sm, status);
     else
         hipLaunchKernelGGL(enc_backward_kernel<1>, dim3(lane_blocks), dim3(kEncBlock), 0, st,
                            (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
-                           states, glen, status);
+                           states, glen, (uint32_t*)sm, status);
     if ((rc = hip_check(hipGetLastError(), "enc_backward_kernel launch"))) return rc;
     hipLaunchKernelGGL(enc_scan_kernel, dim3(1), dim3(1024), 0, st, glen, G, offsets);
     if ((rc = hip_check(hipGetLastError(), "enc_scan_kernel launch"))) return rc;
+    if (N % 16 == 0) return TANS_OK;   // the backward pass wrote the sign/mantissa tiles
     const int64_t sm_blocks = (K + kSmRows - 1) / kSmRows * ((n_tiles + kSmCols - 1) / kSmCols);
     hipLaunchKernelGGL(enc_sm_kernel, dim3((unsigned)sm_blocks), dim3(kEncBlock), 0, st,
                        (const uint8_t*)fp8, K, N, n_tiles, (uint32_t*)sm);
