@@ -337,9 +337,11 @@ __global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
     const uint16_t* __restrict__ chunks, int64_t K, int64_t S,
     const int64_t* __restrict__ offsets, uint32_t* __restrict__ comp) {
     const int lane = threadIdx.x & (kLanes - 1);
-    const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) + threadIdx.x / kLanes;
+    // the group (wave-uniform, so the output resource stays in SGPRs)
+    const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x / kLanes);
     const int64_t G = (K + kLanes - 1) / kLanes;
-    if (g >= G) return;   // wave-uniform
+    if (g >= G) return;
     const int64_t k = g * kLanes + lane;
     const bool active = k < K;
     const int64_t kk = active ? k : K - 1;
@@ -348,23 +350,35 @@ __global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
     const int64_t glen = offsets[g + 1] - base;
     const Rsrc out = __builtin_amdgcn_make_buffer_rsrc(
         comp + base, (short)0, (int)(glen > 0x1FFFFFFF ? 0x7FFFFFFF : glen * 4), 0x00020000);
-    const int64_t n_pairs = (S + 1) / 2;
+    const int n_pairs = (int)((S + 1) / 2);   // S <= 2^24 (checked by the launcher)
     uint64_t acc = 0;   // packed bits not yet stored
     uint32_t n = 0;     // how many
     uint32_t f0 = (uint32_t)lane, f1 = lanes + (uint32_t)lane;   // places of unfinished words
     uint32_t fc = S > 0 && active ? 2u : 0u;                      // how many
     int32_t held = 64;  // bits the lane holds
     uint32_t handed = S > 0 ? 2u * lanes : 0u;
-    for (int64_t q0 = 0; q0 < n_pairs; q0 += kPlaceBatch) {
-        uint32_t c[2 * kPlaceBatch];
+    // the chunks of pairs q0 .. q0 + kPlaceBatch - 1 (zero past step S; the
+    // loads stay in bounds and unconditional, so a batch's loads leave
+    // together), one batch ahead of the packing
+    const uint32_t koff = (uint32_t)kk * 2u;   // K <= INT32_MAX (checked by the launcher)
+    const int steps = (int)S;
+    auto load = [&](uint32_t (&c)[2 * kPlaceBatch], int q0) {
         #pragma unroll
         for (int u = 0; u < 2 * kPlaceBatch; u++) {
-            const int64_t t = 2 * q0 + u;
-            c[u] = t < S ? chunks[t * K + kk] : 0u;   // wave-uniform condition
+            const int t = 2 * q0 + u;
+            const char* row =
+                reinterpret_cast<const char*>(chunks + (int64_t)(t < steps ? t : steps - 1) * K);
+            const uint32_t v = *reinterpret_cast<const uint16_t*>(row + koff);
+            c[u] = t < steps ? v : 0u;   // wave-uniform
         }
+    };
+    uint32_t c[2 * kPlaceBatch], cn[2 * kPlaceBatch];
+    if (n_pairs > 0) load(c, 0);
+    for (int q0 = 0; q0 < n_pairs; q0 += kPlaceBatch) {
+        if (q0 + kPlaceBatch < n_pairs) load(cn, q0 + kPlaceBatch);   // wave-uniform
         #pragma unroll
         for (int u = 0; u < kPlaceBatch; u++) {
-            const int64_t q = q0 + u;
+            const int q = q0 + u;
             if (q >= n_pairs) break;   // wave-uniform
             const uint32_t nb0 = c[2 * u] >> 12, nb1 = c[2 * u + 1] >> 12;
             acc |= (uint64_t)((c[2 * u] & 0xFFFu) | ((c[2 * u + 1] & 0xFFFu) << nb0)) << n;
@@ -392,6 +406,8 @@ __global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
                 handed += (uint32_t)__popcll(m);
             }
         }
+        #pragma unroll
+        for (int u = 0; u < 2 * kPlaceBatch; u++) c[u] = cn[u];
     }
     if (active) {
         if (n > 0) {   // the last, partial word
