@@ -37,8 +37,10 @@ def _compare(T, fp8, hist, alphabet):
                                  (127, 4096), (130, 30), (4096, 14), (300, 208), (70, 48)])
 def test_gpu_encode_matches_cpu(R, alphabet, K, N):
     """N % 16 == 0 takes the backward pass that reads rows in 128-byte blocks
-    (whole blocks at N = 128, 4096; a partial last block at 208, 48, 16);
-    the other widths read one step's bytes at a time."""
+    (whole blocks at N = 128, 4096; a partial last block at 208, 48, 16) and
+    writes the sign/mantissa tiles itself; the other widths read one step's
+    bytes at a time and leave the tiles to enc_sm_kernel.  K % 64 != 0 and
+    K < 64 give groups with lanes out of range; N = 2 (pair) is one step."""
     from rans_vectoradd import tans_codec as T
     _say(f"case: encode_gpu K={K} N={N} {alphabet}")
     torch.manual_seed(42)
