@@ -715,7 +715,12 @@ def main() -> None:
                 "frac_of_2to1_ceiling": raw_gbs / best21},
         "ceiling": ceil | {"best_2to1_gbs": best21, "best_2to1_frac_of_peak": best21 / HBM_PEAK_GBS},
         "memcpy": {"kernel_ms": cpy_kernel, "step_ms": cpy_step,
-                   "gbs": 2 * N_ELEMS / (cpy_step * 1e-3) / 1e9},
+                   "gbs": 2 * N_ELEMS / (cpy_step * 1e-3) / 1e9,
+                   # HBM GB/s of the fused (compressed bytes) and raw kernels as
+                   # fractions of the memcpy rate, the reference's practical ceiling
+                   "fused_frac": (head["hbm_bytes"] / (head["step_ms"] * 1e-3) / 1e9)
+                                 / (2 * N_ELEMS / (cpy_step * 1e-3) / 1e9),
+                   "raw_frac": raw_gbs / (2 * N_ELEMS / (cpy_step * 1e-3) / 1e9)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": read_traffic()},
