@@ -521,7 +521,10 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
     const int64_t S = N / sps;
     const int64_t G = (K + kLanes - 1) / kLanes;
     const int64_t n_tiles = (N + kTile - 1) / kTile;
-    if (K > INT32_MAX || S > (int64_t(1) << 24) || n_tiles * K / kEncBlock + 1 > INT32_MAX)
+    // K within int32 (the kernels' lane offsets) and every grid within the
+    // 32-bit work-item count of a launch
+    const int64_t sm_blocks = (K + kSmRows - 1) / kSmRows * ((n_tiles + kSmCols - 1) / kSmCols);
+    if (K > INT32_MAX || S > (int64_t(1) << 24) || sm_blocks > int64_t(UINT32_MAX) / kEncBlock)
         return fail(TANS_EINVAL, "gpu_encode: tensor too large");
     const WsLayout l = ws_layout(K, S);
     char* ws = static_cast<char*>(workspace);
@@ -541,7 +544,6 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
     hipLaunchKernelGGL(enc_scan_kernel, dim3(1), dim3(1024), 0, st, glen, G, offsets);
     if ((rc = hip_check(hipGetLastError(), "enc_scan_kernel launch"))) return rc;
     if (N % 16 == 0) return TANS_OK;   // the backward pass wrote the sign/mantissa tiles
-    const int64_t sm_blocks = (K + kSmRows - 1) / kSmRows * ((n_tiles + kSmCols - 1) / kSmCols);
     hipLaunchKernelGGL(enc_sm_kernel, dim3((unsigned)sm_blocks), dim3(kEncBlock), 0, st,
                        (const uint8_t*)fp8, K, N, n_tiles, (uint32_t*)sm);
     return hip_check(hipGetLastError(), "enc_sm_kernel launch");

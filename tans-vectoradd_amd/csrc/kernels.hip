@@ -1541,6 +1541,16 @@ int hip_check(hipError_t e, const char* what) {
 
 bool aligned(const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
 
+// A launch's work-item count per grid dimension is a 32-bit number.
+bool grid_fits(int64_t blocks, int64_t threads) {
+    return blocks >= 0 && blocks <= int64_t(UINT32_MAX) / threads;
+}
+
+// The streaming kernels take one 16-byte vector per thread, so one launch
+// covers at most 2^31 vectors (32 GiB per tensor); larger tensors go in
+// several launches on the same stream.
+constexpr int64_t kMaxLaunchVecs = int64_t(1) << 31;
+
 // Compute units of the current device, queried once per device.
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];
@@ -1609,10 +1619,14 @@ int tans_fp8_memcpy(const void* a, void* c, int64_t n, void* stream) {
     if (n == 0) return TANS_OK;
     if (!aligned(a, 16) || !aligned(c, 16)) return fail(TANS_EINVAL, "memcpy: buffers must be 16-byte aligned");
     const int64_t n_vec = n / 16;
-    const int64_t blocks = (n_vec + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL(fp8_copy_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream,
-                       (const v4u*)a, (v4u*)c, n_vec);
-    return hip_check(hipGetLastError(), "fp8_copy_kernel launch");
+    for (int64_t v0 = 0; v0 < n_vec; v0 += kMaxLaunchVecs) {
+        const int64_t m = std::min(kMaxLaunchVecs, n_vec - v0);
+        hipLaunchKernelGGL(fp8_copy_kernel, dim3((unsigned)((m + kBlock - 1) / kBlock)), dim3(kBlock),
+                           0, (hipStream_t)stream, (const v4u*)a + v0, (v4u*)c + v0, m);
+        const int rc = hip_check(hipGetLastError(), "fp8_copy_kernel launch");
+        if (rc != TANS_OK) return rc;
+    }
+    return TANS_OK;
 }
 
 int tans_fp8_vecadd_raw(const void* a, const void* b, void* c, int64_t n, void* stream) {
@@ -1621,10 +1635,15 @@ int tans_fp8_vecadd_raw(const void* a, const void* b, void* c, int64_t n, void* 
     if (!aligned(a, 16) || !aligned(b, 16) || !aligned(c, 16))
         return fail(TANS_EINVAL, "vecadd_raw: buffers must be 16-byte aligned");
     const int64_t n_vec = n / 16;
-    const int64_t blocks = (n_vec + kBlock - 1) / kBlock;
-    hipLaunchKernelGGL(fp8_add_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)stream,
-                       (const v4u*)a, (const v4u*)b, (v4u*)c, n_vec);
-    return hip_check(hipGetLastError(), "fp8_add_kernel launch");
+    for (int64_t v0 = 0; v0 < n_vec; v0 += kMaxLaunchVecs) {
+        const int64_t m = std::min(kMaxLaunchVecs, n_vec - v0);
+        hipLaunchKernelGGL(fp8_add_kernel, dim3((unsigned)((m + kBlock - 1) / kBlock)), dim3(kBlock),
+                           0, (hipStream_t)stream, (const v4u*)a + v0, (const v4u*)b + v0,
+                           (v4u*)c + v0, m);
+        const int rc = hip_check(hipGetLastError(), "fp8_add_kernel launch");
+        if (rc != TANS_OK) return rc;
+    }
+    return TANS_OK;
 }
 
 int tans_stream_probe(int32_t mode, int32_t nontemporal, const void* a, const void* b, void* c,
@@ -1639,20 +1658,28 @@ int tans_stream_probe(int32_t mode, int32_t nontemporal, const void* a, const vo
         (mode == 0 && !aligned(sink, 4)))
         return fail(TANS_EINVAL, "stream_probe: buffers must be 16-byte aligned");
     const int64_t n_vec = n / 16;
-    const dim3 grid((unsigned)((n_vec + kBlock - 1) / kBlock));
-    auto launch = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, (hipStream_t)stream, (const v4u*)a,
-                           (const v4u*)b, (v4u*)c, n_vec, (uint32_t*)sink);
-    };
-    switch (mode * 2 + (nontemporal ? 1 : 0)) {
-        case 0: launch(stream_probe_kernel<0, false>); break;
-        case 1: launch(stream_probe_kernel<0, true>); break;
-        case 2: launch(stream_probe_kernel<1, false>); break;
-        case 3: launch(stream_probe_kernel<1, true>); break;
-        case 4: launch(stream_probe_kernel<2, false>); break;
-        default: launch(stream_probe_kernel<2, true>); break;
+    for (int64_t v0 = 0; v0 < n_vec; v0 += kMaxLaunchVecs) {
+        const int64_t m = std::min(kMaxLaunchVecs, n_vec - v0);
+        const dim3 grid((unsigned)((m + kBlock - 1) / kBlock));
+        const v4u* pa = need_a ? (const v4u*)a + v0 : nullptr;
+        const v4u* pb = need_b ? (const v4u*)b + v0 : nullptr;
+        v4u* pc = need_c ? (v4u*)c + v0 : nullptr;
+        auto launch = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, dim3(kBlock), 0, (hipStream_t)stream, pa, pb, pc, m,
+                               (uint32_t*)sink);
+        };
+        switch (mode * 2 + (nontemporal ? 1 : 0)) {
+            case 0: launch(stream_probe_kernel<0, false>); break;
+            case 1: launch(stream_probe_kernel<0, true>); break;
+            case 2: launch(stream_probe_kernel<1, false>); break;
+            case 3: launch(stream_probe_kernel<1, true>); break;
+            case 4: launch(stream_probe_kernel<2, false>); break;
+            default: launch(stream_probe_kernel<2, true>); break;
+        }
+        const int rc = hip_check(hipGetLastError(), "stream_probe_kernel launch");
+        if (rc != TANS_OK) return rc;
     }
-    return hip_check(hipGetLastError(), "stream_probe_kernel launch");
+    return TANS_OK;
 }
 
 int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs, int32_t nsym,
@@ -1732,7 +1759,7 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
         if (cus <= 0) return fail(TANS_EHIP, "decode: cannot query the device's CU count");
         blocks = std::min<int64_t>(blocks, cus);
     }
-    if (blocks > INT32_MAX) return fail(TANS_EINVAL, "decode: K too large");
+    if (!grid_fits(blocks, kDecBlock)) return fail(TANS_EINVAL, "decode: K too large");
 #define TANS_LAUNCH_DECODE(S)                                                                     \
     hipLaunchKernelGGL((decode_kernel<S>), dim3((unsigned)blocks),                               \
                        dim3(kDecBlock), 0, (hipStream_t)stream, (const uint32_t*)comp,           \
@@ -1801,7 +1828,7 @@ int gemm_fused_launch(const void* comp, int64_t comp_bytes, const int64_t* offse
     const int64_t n_rg = Rp / kGemmGroupRows;
     const int64_t row_blocks = (n_rg + kGemmGroupsPerBlock - 1) / kGemmGroupsPerBlock;
     const int64_t blocks = S * row_blocks;
-    if (blocks > INT32_MAX || B * R / 256 + 1 > INT32_MAX)
+    if (!grid_fits(blocks, kDecBlock) || !grid_fits(B * (Rp / kLanes), kFinWaves * kLanes))
         return fail(TANS_EINVAL, "gemm_fused: matrix too large");
     hipStream_t st = (hipStream_t)stream;
     auto launch = [&](auto kernel) {
@@ -1834,13 +1861,13 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
     if (B == 1) {
         const int64_t rows_per_block = (256 / kLanes) * kRawRows;
         const int64_t blocks = (R + rows_per_block - 1) / rows_per_block;
-        if (blocks > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
+        if (!grid_fits(blocks, 256)) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
         hipLaunchKernelGGL((gemm_raw_dot2_kernel<1>), dim3((unsigned)blocks), dim3(256), 0, st,
                            (const v4u*)w, R, C, (const v4u*)x, scale, (uint16_t*)y);
         return hip_check(hipGetLastError(), "gemm_raw_dot2_kernel launch");
     }
     const int64_t blocks = (R + 15) / 16;
-    if (blocks > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
+    if (!grid_fits(blocks, kRawMaxWaves * kLanes)) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
     // waves per workgroup: enough workgroups x waves to fill the GPU about
     // twice (8192 waves), at most one wave per 64-column block
     int nw = 1;
