@@ -34,6 +34,8 @@ Prints ONE JSON line (progress goes to stderr):
                               gemm|encode  [--alphabet pair|nibble] [--batch B] --steps 5
                                   # one kernel (or the encoder's passes, or one 40-layer
                                   # GEMM pass) only, for rocprofv3
+    python bench.py --profile fused|raw|... --power 4
+                                  # board power and GFX clock while the kernel runs
 """
 from __future__ import annotations
 
@@ -83,6 +85,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--policy", choices=("nt", "default"), default="nt",
                    help="load/store policy of --profile read/write/stream21")
     p.add_argument("--batch", type=int, default=1, help="batch of --profile gemm/gemm_raw")
+    p.add_argument("--power", type=float, default=0.0,
+                   help="with --profile: launch back to back for this many seconds while "
+                        "sampling board power and GFX clock (amd-smi)")
     return p.parse_args()
 
 
@@ -631,12 +636,62 @@ def profile_only(args) -> None:
             dev_args, _, _ = encode_pair(qa, qb, hist, HEADLINE_LANE, args.alphabet)
             fn = lambda: R.fp8_vecadd_fused_tans(*dev_args, HEADLINE_LANE)   # noqa: E731
     n = settle(fn, args.settle)
+    if args.power:
+        print(json.dumps({"profile": args.profile, "power": power_sample(fn, args.power)}))
+        return
     log(f"profile {args.profile}: {n} settle + {args.warmup} warm-up + {args.steps} launches")
     for _ in range(args.warmup + args.steps):
         fn()
     torch.cuda.synchronize()
     print(json.dumps({"profile": args.profile, "settle": n,
                       "launches": n + args.warmup + args.steps}))
+
+
+def power_sample(fn, seconds: float) -> dict:
+    """Launch fn back to back for `seconds` while a thread samples the
+    board (`amd-smi metric -p -c`: socket power and the GFX clock of each
+    XCD); the first second is dropped so the clocks have settled."""
+    import statistics
+    import subprocess
+    import threading
+    import torch
+
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        t0 = time.perf_counter()
+        while not stop.is_set():
+            r = subprocess.run(["amd-smi", "metric", "-g", "0", "-p", "-c", "--json"],
+                               capture_output=True, text=True)
+            t = time.perf_counter() - t0
+            try:
+                g = json.loads(r.stdout)["gpu_data"][0]
+                w = float(g["power"]["socket_power"]["value"])
+                clk = [float(v["clk"]["value"]) for k, v in g["clock"].items()
+                       if k.startswith("gfx_") and isinstance(v, dict)]
+                samples.append((t, w, statistics.median(clk)))
+            except (ValueError, KeyError, IndexError, TypeError):
+                pass
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            fn()
+        n += 20
+        torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    stop.set()
+    th.join()
+    kept = [s for s in samples if s[0] >= 1.0]
+    if not kept:
+        return {"samples": 0, "launches": n}
+    watts, mhz = [s[1] for s in kept], [s[2] for s in kept]
+    return {"samples": len(kept), "launches": n, "seconds": elapsed,
+            "us_per_launch": elapsed / n * 1e6,
+            "socket_w_median": statistics.median(watts), "socket_w_max": max(watts),
+            "gfx_mhz_median": statistics.median(mhz), "gfx_mhz_min": min(mhz)}
 
 
 def main() -> None:
