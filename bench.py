@@ -647,6 +647,20 @@ def profile_only(args) -> None:
                       "launches": n + args.warmup + args.steps}))
 
 
+def parse_amdsmi_metric(text: str):
+    """(socket watts, median GFX MHz over the XCDs) from the JSON of
+    `amd-smi metric -p -c --json` for one GPU, or None if it holds neither."""
+    import statistics
+    try:
+        g = json.loads(text)["gpu_data"][0]
+        w = float(g["power"]["socket_power"]["value"])
+        clk = [float(v["clk"]["value"]) for k, v in g["clock"].items()
+               if k.startswith("gfx_") and isinstance(v, dict)]
+        return w, statistics.median(clk)
+    except (ValueError, KeyError, IndexError, TypeError):
+        return None
+
+
 def power_sample(fn, seconds: float) -> dict:
     """Launch fn back to back for `seconds` while a thread samples the
     board (`amd-smi metric -p -c`: socket power and the GFX clock of each
@@ -661,17 +675,14 @@ def power_sample(fn, seconds: float) -> dict:
     def sampler():
         t0 = time.perf_counter()
         while not stop.is_set():
-            r = subprocess.run(["amd-smi", "metric", "-g", "0", "-p", "-c", "--json"],
-                               capture_output=True, text=True)
-            t = time.perf_counter() - t0
             try:
-                g = json.loads(r.stdout)["gpu_data"][0]
-                w = float(g["power"]["socket_power"]["value"])
-                clk = [float(v["clk"]["value"]) for k, v in g["clock"].items()
-                       if k.startswith("gfx_") and isinstance(v, dict)]
-                samples.append((t, w, statistics.median(clk)))
-            except (ValueError, KeyError, IndexError, TypeError):
-                pass
+                r = subprocess.run(["amd-smi", "metric", "-g", "0", "-p", "-c", "--json"],
+                                   capture_output=True, text=True, timeout=10)
+            except (OSError, subprocess.SubprocessError):
+                return
+            s = parse_amdsmi_metric(r.stdout)
+            if s is not None:
+                samples.append((time.perf_counter() - t0, *s))
 
     th = threading.Thread(target=sampler, daemon=True)
     th.start()
