@@ -21,6 +21,8 @@ Prints ONE JSON line (progress goes to stderr):
                 round of each is reported (all rounds under "rounds")
   roofline      compressed HBM bytes of one fused launch / its duration
                 (HIP events around each launch on the launch stream)
+  power         board power and median GFX clock (amd-smi) while the
+                headline's fused and raw kernels each run back to back
   ceiling       what the raw add's launch shape streams with the arithmetic
                 taken out (read-only, write-only, 2:1 read/write), the raw
                 add's rate as a fraction of the 2:1 ceiling and of 8 TB/s
@@ -57,6 +59,7 @@ HEADLINE_LANE = 1024                 # 64Ki-element streams
 DECODE_ELEMS = 1 << 30               # config 2
 SWEEP_LANES = (16, 64, 256, 1024)    # 1Ki, 4Ki, 16Ki, 64Ki streams
 SETTLE_S = 0.3                       # seconds of back-to-back calls before timing
+POWER_S = 3.0                        # seconds of power/clock sampling per headline kernel
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fused_vecadd_64ki_pair_traffic.txt")
 
 
@@ -76,6 +79,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-decode", action="store_true", help="skip config 2 (standalone decode)")
     p.add_argument("--no-gemm", action="store_true", help="skip configs 3-4 (decode-GEMV/GEMM)")
+    p.add_argument("--no-power", action="store_true",
+                   help="skip sampling board power and GFX clock under the headline kernels")
     p.add_argument("--alphabet", choices=("pair", "nibble"), default="pair",
                    help="alphabet of --profile fused/decode")
     p.add_argument("--profile", choices=("fused", "raw", "memcpy", "read", "write", "stream21",
@@ -198,12 +203,14 @@ def gpu_encode_rate(q_d, hist, lane: int, alphabet: str, reps: int = 5) -> dict:
 
 
 def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps: int,
-                     warmup: int, settle_s: float, raw_fn=None, rounds: int = 1) -> dict:
+                     warmup: int, settle_s: float, raw_fn=None, rounds: int = 1,
+                     power_s: float = 0.0) -> dict:
     """One fused configuration.  With raw_fn, the raw kernel and the fused
     one are timed in alternation for `rounds` rounds of `steps` launches each
     (raw first), so both see the same clocks and board temperature; the
     round with the median fused step time is reported, with the median raw
-    round beside it."""
+    round beside it.  With power_s > 0 as well, board power and GFX clock
+    are then sampled while each runs back to back for power_s seconds."""
     import torch
     import rans_vectoradd as R
 
@@ -231,6 +238,9 @@ def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps:
         extra = {"raw_kernel_ms": raw_kernel, "raw_step_ms": raw_step,
                  "rounds_step_ms": [r[1] for r in fused_rounds],
                  "raw_rounds_step_ms": [r[1] for r in raw_rounds]}
+        if power_s > 0:
+            extra["power"] = {"seconds_each": power_s, "fused": power_sample(fn, power_s),
+                              "raw": power_sample(raw_fn, power_s)}
     del args
     torch.cuda.empty_cache()
     return extra | {"stream_elems": 64 * lane, "lane_elems": lane, "alphabet": alphabet,
@@ -734,9 +744,14 @@ def main() -> None:
         log(f"fused: stream {64 * lane} elements ({lane} per lane), {alph}"
             + ("; raw and fused timed in alternation, 3 rounds" if i == 0 else ""))
         r = run_fused_config(qa, qb, raw_out, hist, lane, alph, args.steps, args.warmup,
-                             args.settle, raw_fn=raw_fn if i == 0 else None, rounds=3)
+                             args.settle, raw_fn=raw_fn if i == 0 else None, rounds=3,
+                             power_s=0.0 if args.no_power else POWER_S)
         if i == 0:
             raw_kernel, raw_step = r["raw_kernel_ms"], r["raw_step_ms"]
+            for k, v in (r.get("power") or {}).items():
+                if isinstance(v, dict) and v.get("samples"):
+                    log(f"  {k}: {v['socket_w_median']:.0f} W, GFX {v['gfx_mhz_median']:.0f} MHz "
+                        f"({v['samples']} samples)")
         results.append(r)
         log(f"  kernel {r['kernel_ms'] * 1e3:.1f} us  step {r['step_ms'] * 1e3:.1f} us  "
             f"x_raw {raw_step / r['step_ms']:.3f}  bits/B {r['bits_per_byte']:.3f}  "
@@ -776,6 +791,7 @@ def main() -> None:
         "compressed_hbm_gbs": achieved,
         "rounds": {"fused_step_ms": head["rounds_step_ms"],
                    "raw_step_ms": head["raw_rounds_step_ms"]},
+        "power": head.get("power"),
         "raw": {"kernel_ms": raw_kernel, "step_ms": raw_step, "gbs": raw_gbs,
                 "frac_of_peak": raw_gbs / HBM_PEAK_GBS,
                 "frac_of_2to1_ceiling": raw_gbs / best21},
