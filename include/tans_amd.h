@@ -18,20 +18,25 @@
  *     wave64 (lane j of the group = wave lane j).
  *   - Symbols: the exponent nibble e = (b >> 3) & 15.  Pair alphabet: one
  *     symbol e0*16+e1 per two elements, table of 2^12 states.  Nibble
- *     alphabet: one symbol per element, 2^11 states.  The table size fixes
- *     the alphabet.
+ *     alphabet: one symbol per element, 2^11 states, every present
+ *     symbol's frequency at least 2.  The table size fixes the alphabet.
  *   - Bitstream: each lane's bits, in decode order, are cut into u32 words
  *     read LSB first; every decode step reads nb bits as one value.  The
  *     words of the 64 lanes of group g form one stream at
  *     comp_words[offsets[g] ..], ordered by the refill schedule all decoders
  *     follow: every active lane starts with two words (the stream's first
- *     words go to lanes 0, 1, ... in turn, then their second words); after
- *     each step pair (steps 2p, 2p + 1) except the last, each active lane
- *     holding at most 32 unread bits takes the next stream word (lanes in
- *     ascending order) and gains 32 bits; after the second-to-last pair only
- *     a lane holding fewer than 24 bits does.  Streams start on 16-byte
- *     boundaries; 1 KiB of zero words follows the last one.  offsets is
- *     int64 [n_groups + 1], in words.
+ *     words go to lanes 0, 1, ... in turn, then their second words).  The
+ *     steps are cut into segments: step pairs (2p, 2p + 1) with 2^12-state
+ *     tables; with 2^11-state tables, steps 8s .. 8s + 2, 8s + 3 .. 8s + 5
+ *     and 8s + 6, 8s + 7 of every 8 (such tables give every present symbol
+ *     a frequency of at least 2, so no step reads more than 10 bits).
+ *     After each segment except the last, each active lane holding at most
+ *     32 unread bits takes the next stream word (lanes in ascending order)
+ *     and gains 32 bits; after the second-to-last segment only a lane
+ *     holding fewer bits than the last segment can read does (24 with
+ *     2^12-state tables, 10 per step of the last segment with 2^11).
+ *     Streams start on 16-byte boundaries; 1 KiB of zero words follows the
+ *     last one.  offsets is int64 [n_groups + 1], in words.
  *   - states[k] is lane k's initial decoder state in [L, 2L).
  *   - Sign/mantissa nibbles: 16-element tiles, 8 bytes per (tile, lane) at
  *     sm[(t * K + k) * 8]; u32 word h covers elements 8h..8h+7 as

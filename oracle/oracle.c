@@ -374,10 +374,15 @@ int ora_ref_decode_add(const uint8_t* a_comp8, const int32_t* a_off, const uint1
  *   (LSB = earliest bit); each decode step reads nb bits as one value.
  *   Group g's words form one stream at comp_words[offsets[g] ..], in the
  *   order of this refill schedule: first every active lane (ascending j)
- *   takes one word, then every active lane takes a second; after each step
- *   pair (steps 2p, 2p+1) except the last, each active lane (ascending j)
- *   holding at most 32 unread bits takes the next stream word (+32 bits),
- *   and after the second-to-last pair only a lane holding fewer than 24.
+ *   takes one word, then every active lane takes a second; the steps are
+ *   cut into segments, and after each segment except the last, each active
+ *   lane (ascending j) holding at most 32 unread bits takes the next stream
+ *   word (+32 bits); after the second-to-last segment only a lane holding
+ *   fewer bits than the last segment can read does.  Segments: with
+ *   2^11-state tables (whose symbols all have f >= 2, so nb <= 10), every 8
+ *   steps are cut into 3, 3 and 2 steps, and the last segment can read
+ *   10 bits per step; with other tables, step pairs (2p, 2p+1), and the
+ *   last one can read 24 bits.
  *   states[k] is the initial decoder state in [L, 2L).
  *   Symbols: sps=2 -> pair symbol e0*16+e1 per step; sps=1 -> one exponent.
  *   Sign/mantissa: tiles of 16 elements, 8 bytes per (tile, lane) at
@@ -475,7 +480,13 @@ int ora_w64_decode(const uint8_t* comp8, const int64_t* offsets, const uint16_t*
                     if (lane_take(&ln[j], comp[pos++])) bad = -15;
                 }
         }
-        const int64_t pairs = (steps + 1) / 2;
+        /* segment of each step and the number of segments (see above) */
+        const int triple = (log2L == 11);
+        #define SEG_OF(i) (triple ? 3 * ((i) / 8) + ((i) % 8 < 3 ? 0 : (i) % 8 < 6 ? 1 : 2) : (i) / 2)
+        const int64_t n_seg = steps > 0 ? SEG_OF(steps - 1) + 1 : 0;
+        int64_t last_start = steps - 1;       /* first step of the last segment */
+        while (last_start > 0 && SEG_OF(last_start - 1) == n_seg - 1) last_start--;
+        const uint64_t final_below = triple ? (uint64_t)(10 * (steps - last_start)) : 24;
         for (int64_t i = 0; i < steps && !bad; i++) {
             for (int j = 0; j < lanes && !bad; j++) {
                 int64_t k = g * 64 + j;
@@ -489,9 +500,10 @@ int ora_w64_decode(const uint8_t* comp8, const int64_t* offsets, const uint16_t*
                 if (sps == 2)
                     out[k * N + el + 1] = compose_fp8((uint32_t)e1, sm_nibble_of(sm8, (int)((el + 1) % 16)));
             }
-            const int64_t p = i / 2;
-            if ((i % 2 == 1 || i == steps - 1) && p + 1 < pairs) {
-                const uint64_t below = (p + 2 == pairs) ? 24 : 33;
+            const int64_t p = SEG_OF(i);
+            const int seg_end = i == steps - 1 || SEG_OF(i + 1) != p;
+            if (seg_end && p + 1 < n_seg) {
+                const uint64_t below = (p + 2 == n_seg) ? final_below : 33;
                 for (int j = 0; j < lanes && !bad; j++) {
                     uint64_t avail = (uint64_t)ln[j].n_words * 32 - ln[j].rd;
                     if (avail < below) {
@@ -501,6 +513,7 @@ int ora_w64_decode(const uint8_t* comp8, const int64_t* offsets, const uint16_t*
                 }
             }
         }
+        #undef SEG_OF
         for (int j = 0; j < lanes && !bad; j++) {
             if (ln[j].x != L) { bad = -11; break; }
             for (uint64_t p = ln[j].rd; p < (uint64_t)ln[j].n_words * 32; p++)

@@ -12,6 +12,7 @@
 // refills hit a few adjacent 256-byte rows.  There is no partial-slab count:
 // a lane's bitstream starts at bit 0 of its first word.
 #include "../../include/tans_amd.h"
+#include "schedule.h"
 
 #include <algorithm>
 #include <cstdint>
@@ -38,15 +39,14 @@ inline uint32_t rotl32(uint32_t v, int r) { return (v << r) | (v >> (32 - r)); }
 
 inline int ilog2(uint32_t v) { return 31 - __builtin_clz(v); }
 
-// Refill schedule shared with the decoders: every lane starts with two
-// 32-bit words of its group's stream (the first words of lanes 0, 1, ...,
-// then their second words).  After each step pair (steps 2p, 2p + 1) but the
-// last, a lane holding at most 32 unread bits takes the next word (lanes in
-// ascending order); after the second-to-last pair only a lane holding fewer
-// than 24 does.  Two steps read at most 2 * 12 bits, so the 64-bit buffer
-// never runs dry and never overflows.
-constexpr int kRefillAtMost = 32;
-constexpr int kRefillFinalBelow = 24;
+// Refill schedule shared with the decoders (schedule.h): every lane starts
+// with two 32-bit words of its group's stream (the first words of lanes 0,
+// 1, ..., then their second words).  After each segment of steps but the
+// last (two steps; three, three and two with 2^11-state tables), a lane
+// holding at most 32 unread bits takes the next word (lanes in ascending
+// order); after the second-to-last segment only a lane holding fewer bits
+// than the last segment can read does.  A segment reads at most 30 bits, so
+// the 64-bit buffer never runs dry and never overflows.
 // Zero words appended after the last group, so 16-byte segment loads near
 // the end stay inside the buffer.
 constexpr int64_t kTailWords = 256;
@@ -63,9 +63,13 @@ int build_enc_tables(const int32_t* freqs, int32_t nsym, const int32_t* spread,
     t.start.assign(nsym, 0);
     t.freq.assign(nsym, 0);
     t.next.assign(L, 0);
+    const bool triple = log2L == tans_sched::kTripleLog2L;
     uint64_t sum = 0;
     for (int s = 0; s < nsym; s++) {
         if (freqs[s] < 0) return fail(TANS_ETABLE, "negative frequency");
+        if (triple && freqs[s] > 0 && (uint32_t)freqs[s] < tans_sched::kTripleMinFreq)
+            return fail(TANS_ETABLE, "tables of 2^11 states need every present symbol's "
+                                     "frequency >= 2 (nb <= 10)");
         t.start[s] = (uint32_t)sum;
         t.freq[s] = (uint32_t)freqs[s];
         sum += (uint32_t)freqs[s];
@@ -267,13 +271,16 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
                 for (int r = 0; r < 2; r++)
                     for (int j = 0; j < lanes; j++) take(j);
             }
-            const int64_t n_pairs = (S + 1) / 2;
-            for (int64_t q = 0; q + 1 < n_pairs; q++) {
-                const int32_t below = (q + 2 == n_pairs) ? kRefillFinalBelow : kRefillAtMost + 1;
+            const bool triple = log2L == tans_sched::kTripleLog2L;
+            const int64_t n_seg = tans_sched::segments(S, triple);
+            for (int64_t q = 0; q + 1 < n_seg; q++) {
+                const int32_t below = (q + 2 == n_seg) ? tans_sched::final_below(S, triple)
+                                                        : tans_sched::kAtMost + 1;
+                const int64_t i0 = tans_sched::seg_start(q, triple);
+                const int64_t i1 = tans_sched::seg_start(q + 1, triple);
                 for (int j = 0; j < lanes; j++) {
                     const uint32_t* ch = chunk.data() + j * S;
-                    cnt[j] -= (int32_t)(ch[2 * q] >> 16);
-                    if (2 * q + 1 < S) cnt[j] -= (int32_t)(ch[2 * q + 1] >> 16);
+                    for (int64_t i = i0; i < i1; i++) cnt[j] -= (int32_t)(ch[i] >> 16);
                     if (cnt[j] < below) take(j);
                 }
             }

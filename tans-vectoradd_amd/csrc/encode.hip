@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "../../include/tans_amd.h"
+#include "schedule.h"
 
 extern "C" void tans_internal_set_error(const char* msg);  // codec.cpp
 
@@ -35,8 +36,6 @@ namespace {
 
 constexpr int kLanes = 64;
 constexpr int kTile = 16;
-constexpr int kRefillAtMost = 32;      // the decoders' refill rule: take at <= 32 unread bits
-constexpr int kRefillFinalBelow = 24;  // after the second-to-last step pair: below 24
 constexpr int64_t kTailWords = 256;
 constexpr int kEncBlock = 256;
 
@@ -178,28 +177,30 @@ __device__ __forceinline__ void load_block(v4u (&b)[kEncBlockChunks], const v4u*
     }
 }
 
-// The refill schedule: every lane in range starts with two words (64 bits);
-// steps 2q and 2q + 1 consume their nb bits, and after that step pair, if it
-// is not the last, a lane holding at most 32 bits takes the next word (+32
-// bits); after the second-to-last pair only a lane holding fewer than 24
-// does.  A pair consumes at most 24 bits, so after every check but the final
-// one a lane holds 33..64 bits: with c the bits consumed so far it has taken
-// floor(c / 32) + 2 words.  The words a lane takes in all are therefore
-// fixed by its bit count up to the third-to-last pair (c3) and up to the
-// second-to-last (c2): t = floor(c3 / 32) + 2, plus one when 32 t - c2 < 24
-// (t = 2, c3 = 0 with two pairs; 2 words with one pair; none for S = 0).
-// The walk records its bit count after the last pair (b1: bits of steps
-// 2 (n - 1) ..) and after the second-to-last (b2: steps 2 (n - 2) ..), so
-// c2 = bits - b1 and c3 = bits - b2.
-__device__ __forceinline__ uint32_t lane_words(int64_t S, uint32_t bits, uint32_t b1,
-                                               uint32_t b2) {
+// The refill schedule (schedule.h): every lane in range starts with two
+// words (64 bits); each segment of steps (2 steps, or 3, 3, 2 per 8 with
+// 2^11-state tables) consumes its nb bits, and after a segment that is not
+// the last, a lane holding at most 32 bits takes the next word (+32 bits);
+// after the second-to-last segment only a lane holding fewer bits than the
+// last segment can read (final_below) does.  A segment consumes at most 30
+// bits, so after every check but the final one a lane holds 33..64 bits:
+// with c the bits consumed so far it has taken floor(c / 32) + 2 words.
+// The words a lane takes in all are therefore fixed by its bit count up to
+// the third-to-last segment (c3) and up to the second-to-last (c2):
+// t = floor(c3 / 32) + 2, plus one when 32 t - c2 < final_below (t = 2,
+// c3 = 0 with two segments; 2 words with one segment; none for S = 0).  The
+// walk records its bit count after the last segment (b1: bits of the last
+// segment's steps) and after the second-to-last (b2: the last two
+// segments'), so c2 = bits - b1 and c3 = bits - b2.
+__device__ __forceinline__ uint32_t lane_words(int64_t S, bool triple, uint32_t bits,
+                                               uint32_t b1, uint32_t b2) {
     if (S == 0) return 0u;
-    const int64_t n = (S + 1) / 2;   // step pairs
+    const int64_t n = tans_sched::segments(S, triple);
     if (n == 1) return 2u;
     const uint32_t c2 = bits - b1;
     const uint32_t c3 = n >= 3 ? bits - b2 : 0u;
     const uint32_t t = c3 / 32u + 2u;
-    return t + (32u * t - c2 < (uint32_t)kRefillFinalBelow ? 1u : 0u);
+    return t + (32u * t - c2 < (uint32_t)tans_sched::final_below(S, triple) ? 1u : 0u);
 }
 
 // One thread per lane walks its row backwards.  When rows are 16-byte
@@ -227,18 +228,21 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     const int64_t k = (int64_t)blockIdx.x * kEncBlock + threadIdx.x;
     if (k - (threadIdx.x & (kLanes - 1)) >= K) return;   // the whole group is out of range
     const int64_t S = N / SPS;
+    constexpr bool kTriple = SPS == 1;   // 2^11-state tables: 3-3-2 segments
     uint32_t words = 0;
     if (k < K) {
         const int64_t row = k * N;
         uint32_t x = L;
         uint32_t bad = 0;    // bit 31: a symbol of frequency 0
         uint32_t bits = 0;          // the lane's stream bits
-        uint32_t b1 = 0, b2 = 0;    // bits of the last pair, of the last two (lane_words)
+        uint32_t b1 = 0, b2 = 0;    // bits of the last segment, of the last two (lane_words)
         const uint32_t koff = (uint32_t)k * 2u;   // K <= INT32_MAX (checked by the launcher)
         if (N % 16 == 0) {   // kernel-uniform
-            // S is a multiple of 8, so the last two pairs are the first four
-            // steps of the walk, all in the row's last chunk
+            // S is a multiple of 8 (pair) or 16 (nibble), so the last two
+            // segments (steps S - 4 .. or S - 5 ..) are the walk's first
+            // steps, all in the row's last chunk
             constexpr int kQ = 16 / SPS;   // steps per chunk
+            constexpr int kB2 = kTriple ? kQ - 5 : kQ - 4;   // first step of the last two
             const v4u* rp = reinterpret_cast<const v4u*>(fp8 + row);
             const int64_t nch = N / 16;
             v4u cur[kEncBlockChunks], nxt[kEncBlockChunks];
@@ -255,7 +259,7 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
                                  j * kQ + q, K, koff);
                         if constexpr (q == kQ - 2) {
                             if (j == nch - 1) b1 = bits;   // wave-uniform
-                        } else if constexpr (q == kQ - 4) {
+                        } else if constexpr (q == kB2) {
                             if (j == nch - 1) b2 = bits;
                         }
                     });
@@ -270,17 +274,20 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
                 for (int c = 0; c < kEncBlockChunks; c++) cur[c] = nxt[c];
             }
         } else {
-            const int64_t last = 2 * ((S + 1) / 2 - 1);   // first step of the last pair
+            // first steps of the last segment and of the one before it
+            const int64_t n_seg = tans_sched::segments(S, kTriple);
+            const int64_t last = tans_sched::seg_start(n_seg - 1, kTriple);
+            const int64_t last2 = n_seg >= 2 ? tans_sched::seg_start(n_seg - 2, kTriple) : -1;
             for (int64_t i = S - 1; i >= 0; i--) {
                 enc_step(symbol_at<SPS>(fp8, row + i * SPS, K * N), tab, nx, L, x, bad, bits,
                          chunks, i, K, koff);
                 if (i == last) b1 = bits;
-                if (i == last - 2) b2 = bits;
+                if (i == last2) b2 = bits;
             }
         }
         states[k] = (uint16_t)x;
         if (bad >> 31) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
-        words = lane_words(S, bits, b1, b2);
+        words = lane_words(S, kTriple, bits, b1, b2);
     }
     #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) words += __shfl_xor(words, m, kLanes);
@@ -324,18 +331,25 @@ __global__ __launch_bounds__(kEncBlock) void zero_words_kernel(uint32_t* __restr
 // chunks into 32-bit words, LSB first.  A word's place in the stream is
 // fixed when the lane takes it: the first two words of every lane are the
 // first 2 x lanes words (first words in lane order, then the second), and
-// a word taken after a step pair goes to handed + rank (ballot + mbcnt,
-// the order the decoders read it).  A word is stored when its last bit is
-// packed, which comes after it is taken (a pair adds at most 24 bits, and
-// a lane takes a word only once it holds at most 32), so each lane keeps
-// the places of at most two taken, unfinished words.  Words taken past the
-// lane's bits, and the group's padding to 4 words, are zero.  The stores go
-// through a buffer resource bounded by the group's length.
-constexpr int kPlaceBatch = 8;   // step pairs whose chunks are loaded together
+// a word taken after a segment goes to handed + rank (ballot + mbcnt, the
+// order the decoders read it).  A word is stored when its last bit is
+// packed, which comes after it is taken (a segment adds at most 30 bits,
+// and a lane takes a word only once it holds at most 32), so each lane
+// keeps the places of at most two taken, unfinished words.  Words taken
+// past the lane's bits, and the group's padding to 4 words, are zero.  The
+// stores go through a buffer resource bounded by the group's length.
+// TRIPLE: 2^11-state tables, segments of 3, 3, 2 steps (schedule.h).
+constexpr int kPlaceSteps = 16;   // steps whose chunks are loaded together (whole segments)
 
+template <bool TRIPLE>
 __global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
     const uint16_t* __restrict__ chunks, int64_t K, int64_t S,
     const int64_t* __restrict__ offsets, uint32_t* __restrict__ comp) {
+    // segments per kPlaceSteps steps, and their first steps and lengths
+    constexpr int kSegs = TRIPLE ? 6 : 8;
+    constexpr auto seg_first = [](int q) { return TRIPLE ? 8 * (q / 3) + 3 * (q % 3) : 2 * q; };
+    constexpr auto seg_len = [](int q) { return TRIPLE ? (q % 3 == 2 ? 2 : 3) : 2; };
+    static_assert(seg_first(kSegs - 1) + seg_len(kSegs - 1) == kPlaceSteps, "whole segments");
     const int lane = threadIdx.x & (kLanes - 1);
     // the group (wave-uniform, so the output resource stays in SGPRs)
     const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) +
@@ -350,41 +364,47 @@ __global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
     const int64_t glen = offsets[g + 1] - base;
     const Rsrc out = __builtin_amdgcn_make_buffer_rsrc(
         comp + base, (short)0, (int)(glen > 0x1FFFFFFF ? 0x7FFFFFFF : glen * 4), 0x00020000);
-    const int n_pairs = (int)((S + 1) / 2);   // S <= 2^24 (checked by the launcher)
+    // S <= 2^24 (checked by the launcher)
+    const int n_seg = (int)tans_sched::segments(S, TRIPLE);
+    const int32_t fin_below = S > 0 ? tans_sched::final_below(S, TRIPLE) : 0;
     uint64_t acc = 0;   // packed bits not yet stored
     uint32_t n = 0;     // how many
     uint32_t f0 = (uint32_t)lane, f1 = lanes + (uint32_t)lane;   // places of unfinished words
     uint32_t fc = S > 0 && active ? 2u : 0u;                      // how many
     int32_t held = 64;  // bits the lane holds
     uint32_t handed = S > 0 ? 2u * lanes : 0u;
-    // the chunks of pairs q0 .. q0 + kPlaceBatch - 1 (zero past step S; the
+    // the chunks of steps t0 .. t0 + kPlaceSteps - 1 (zero past step S; the
     // loads stay in bounds and unconditional, so a batch's loads leave
     // together), one batch ahead of the packing
     const uint32_t koff = (uint32_t)kk * 2u;   // K <= INT32_MAX (checked by the launcher)
     const int steps = (int)S;
-    auto load = [&](uint32_t (&c)[2 * kPlaceBatch], int q0) {
+    auto load = [&](uint32_t (&c)[kPlaceSteps], int t0) {
         #pragma unroll
-        for (int u = 0; u < 2 * kPlaceBatch; u++) {
-            const int t = 2 * q0 + u;
+        for (int u = 0; u < kPlaceSteps; u++) {
+            const int t = t0 + u;
             const char* row =
                 reinterpret_cast<const char*>(chunks + (int64_t)(t < steps ? t : steps - 1) * K);
             const uint32_t v = *reinterpret_cast<const uint16_t*>(row + koff);
             c[u] = t < steps ? v : 0u;   // wave-uniform
         }
     };
-    uint32_t c[2 * kPlaceBatch], cn[2 * kPlaceBatch];
-    if (n_pairs > 0) load(c, 0);
-    for (int q0 = 0; q0 < n_pairs; q0 += kPlaceBatch) {
-        if (q0 + kPlaceBatch < n_pairs) load(cn, q0 + kPlaceBatch);   // wave-uniform
+    uint32_t c[kPlaceSteps], cn[kPlaceSteps];
+    if (steps > 0) load(c, 0);
+    for (int t0 = 0; t0 < steps; t0 += kPlaceSteps) {
+        if (t0 + kPlaceSteps < steps) load(cn, t0 + kPlaceSteps);   // wave-uniform
+        const int j0 = t0 / kPlaceSteps * kSegs;
         #pragma unroll
-        for (int u = 0; u < kPlaceBatch; u++) {
-            const int q = q0 + u;
-            if (q >= n_pairs) break;   // wave-uniform
-            const uint32_t nb0 = c[2 * u] >> 12, nb1 = c[2 * u + 1] >> 12;
-            acc |= (uint64_t)((c[2 * u] & 0xFFFu) | ((c[2 * u + 1] & 0xFFFu) << nb0)) << n;
-            n += nb0 + nb1;
-            held -= (int32_t)(nb0 + nb1);
-            if (n >= 32) {   // at most one word per pair (n < 32 + 24)
+        for (int q = 0; q < kSegs; q++) {
+            const int j = j0 + q;
+            if (j >= n_seg) break;   // wave-uniform
+            #pragma unroll
+            for (int u = seg_first(q); u < seg_first(q) + seg_len(q); u++) {
+                const uint32_t nb = c[u] >> 12;
+                acc |= (uint64_t)(c[u] & 0xFFFu) << n;
+                n += nb;
+                held -= (int32_t)nb;
+            }
+            if (n >= 32) {   // at most one word per segment (n < 32 + 30)
                 if (active)
                     __builtin_amdgcn_raw_buffer_store_b32((uint32_t)acc, out, f0 * 4u, 0, 0);
                 f0 = f1;
@@ -392,8 +412,8 @@ __global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
                 acc >>= 32;
                 n -= 32;
             }
-            if (q + 1 < n_pairs) {   // wave-uniform: no check after the last pair
-                const int32_t below = q + 2 == n_pairs ? kRefillFinalBelow : kRefillAtMost + 1;
+            if (j + 1 < n_seg) {   // wave-uniform: no check after the last segment
+                const int32_t below = j + 2 == n_seg ? fin_below : tans_sched::kAtMost + 1;
                 const bool need = active && held < below;
                 const Mask m = __ballot(need);
                 const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
@@ -407,7 +427,7 @@ __global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
             }
         }
         #pragma unroll
-        for (int u = 0; u < 2 * kPlaceBatch; u++) c[u] = cn[u];
+        for (int u = 0; u < kPlaceSteps; u++) c[u] = cn[u];
     }
     if (active) {
         if (n > 0) {   // the last, partial word
@@ -566,10 +586,14 @@ int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* work
         const int64_t G = (K + kLanes - 1) / kLanes;
         const WsLayout l = ws_layout(K, S);
         const char* ws = static_cast<const char*>(workspace);
-        hipLaunchKernelGGL(enc_place_kernel,
-                           dim3((unsigned)((G + kEncBlock / kLanes - 1) / (kEncBlock / kLanes))),
-                           dim3(kEncBlock), 0, st, reinterpret_cast<const uint16_t*>(ws + l.chunks),
-                           K, S, offsets, c32);
+        const dim3 grid((unsigned)((G + kEncBlock / kLanes - 1) / (kEncBlock / kLanes)));
+        const uint16_t* ch = reinterpret_cast<const uint16_t*>(ws + l.chunks);
+        if (sps == 1)   // 2^11-state tables: the 3-3-2 schedule
+            hipLaunchKernelGGL(enc_place_kernel<true>, grid, dim3(kEncBlock), 0, st, ch, K, S,
+                               offsets, c32);
+        else
+            hipLaunchKernelGGL(enc_place_kernel<false>, grid, dim3(kEncBlock), 0, st, ch, K, S,
+                               offsets, c32);
         if ((rc = hip_check(hipGetLastError(), "enc_place_kernel launch"))) return rc;
     }
     hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((kTailWords + kEncBlock - 1) / kEncBlock)),

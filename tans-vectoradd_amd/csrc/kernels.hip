@@ -23,27 +23,28 @@
 // tANS state.  The decode table lives in LDS as 8-byte entries addressed by
 // a byte offset kept in the state register.  A lane's unread bits sit in a
 // 64-bit window (hi:lo) read from bit pos of lo (0 <= pos < 32).  Steps go
-// in pairs: one funnel shift takes the 32 bits from pos (two steps read at
-// most 24), each step is a ds_read_b64 of the entry, a bit-field extract of
-// nb bits and one shift-add for the next entry's offset, and pos advances
-// by nb1 + nb2 in a register that holds pos both in bits 4:0 and in bits
-// 31:27 (the table holds nb in both places), so the add's carry out is set
-// exactly when lo is used up.
+// in segments (schedule.h): pairs with the pair alphabet, 3, 3 and 2 steps
+// per 8 with the nibble alphabet.  One funnel shift takes the 32 bits from
+// pos (a segment reads at most 24 or 30), each step is a ds_read_b64 of the
+// entry, a bit-field extract of nb bits and one shift-add for the next
+// entry's offset, and pos advances by the segment's nb sum in a register
+// that holds pos both in bits 4:0 and in bits 31:27 (the table holds nb in
+// both places), so the add's carry out is set exactly when lo is used up.
 //
-// That carry drives the refill: after each step pair but the last, the
-// lanes whose lo is used up move hi into lo and take the next word of the
-// group's stream (the carry mask, an mbcnt for each lane's rank and one
-// ds_read_b32 from the wave's LDS ring); after the second-to-last pair a
-// lane takes a word only below 24 unread bits.  Each lane starts with two
-// words.  The ring holds kSlots segments of 256 words (one 16-byte load per
+// That carry drives the refill: after each segment but the last, the lanes
+// whose lo is used up move hi into lo and take the next word of the group's
+// stream (the carry mask, an mbcnt for each lane's rank and one ds_read_b32
+// from the wave's LDS ring); after the second-to-last segment a lane takes
+// a word only when it holds fewer bits than the last segment can read.
+// Each lane starts with two words.  The ring holds kSlots segments of 256 words (one 16-byte load per
 // lane) plus a 64-word mirror of its first words, so a wave's 64
 // consecutive reads never wrap.  A stage issues at most one segment load
 // per stream, through a buffer resource whose base is the stream's first
 // word and whose bound is the buffer's end, once the segment's ring slot is
 // free.  The loaded segment stays in registers and is written into the
 // ring at the next stage whose slot is free, which comes no later than the
-// stage in which a lane could first take one of its words.  A stage is four
-// refill checks, so at most 256 words are handed out per stage, and
+// stage in which a lane could first take one of its words.  A stage is at
+// most four refill checks, so at most 256 words are handed out per stage, and
 // kSlots = kDelay + 2 slots guarantee that a fetched segment starts more
 // than a stage's worth of words ahead of the lanes.  Lanes out of range
 // (a tensor's last, partial group) step on a sink table entry that reads
@@ -63,6 +64,7 @@
 #include <type_traits>
 
 #include "../../include/tans_amd.h"
+#include "schedule.h"
 
 extern "C" void tans_internal_set_error(const char* msg);  // codec.cpp
 
@@ -285,7 +287,7 @@ __device__ __forceinline__ Rsrc rsrc(const void* base, uint32_t bytes) {
 // ---------------------------------------------------------------------
 typedef v4u Seg;                           // one segment: 16 bytes per lane
 constexpr int kSegWords = 4 * kLanes;
-constexpr int kChecksPerStage = 4;         // a stage is 4 refill checks (8 steps)
+constexpr int kChecksPerStage = 4;         // at most 4 refill checks per stage (8 steps)
 constexpr int kDelay = 1;                  // stages from a segment load to its earliest ring write
 constexpr int kSlots = kDelay + 2;
 constexpr int kRingWords = kSlots * kSegWords;
@@ -446,6 +448,29 @@ __device__ __forceinline__ Mask dec_pair(Lane& l, const v2u* __restrict__ tbl, u
     return add_carry(l.q, e1.x + e2.x);
 }
 
+// Three tANS steps from one funnel shift (tables of 2^11 states, nb <= 10:
+// at most 30 bits).  The third step's field starts at nb1 + nb2, the low
+// bits of word0_1 + word0_2 (at most 20, so the exponent bits above them
+// are untouched); q advances by nb1 + nb2 + nb3 < 32 in both copies.
+__device__ __forceinline__ Mask dec_triple(Lane& l, const v2u* __restrict__ tbl, uint32_t& w1,
+                                           uint32_t& w2, uint32_t& w3) {
+    const uint32_t t = __builtin_amdgcn_alignbit(l.hi, l.lo, l.q);   // shift = q[4:0]
+    const v2u e1 = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
+    const uint32_t b1 = __builtin_amdgcn_ubfe(t, 0u, e1.x);           // width = nb1
+    l.x8 = (b1 << 3) + e1.y;
+    const v2u e2 = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
+    const uint32_t b2 = __builtin_amdgcn_ubfe(t, e1.x, e2.x);          // offset nb1, width nb2
+    l.x8 = (b2 << 3) + e2.y;
+    const uint32_t s12 = e1.x + e2.x;
+    const v2u e3 = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
+    const uint32_t b3 = __builtin_amdgcn_ubfe(t, s12, e3.x);           // offset nb1 + nb2
+    l.x8 = (b3 << 3) + e3.y;
+    w1 = e1.x;
+    w2 = e2.x;
+    w3 = e3.x;
+    return add_carry(l.q, s12 + e3.x);
+}
+
 // (c << 2) + b in one SALU instruction (s_lshl2_add_u32, which sets SCC).
 __device__ __forceinline__ uint32_t lshl2_add(uint32_t c, uint32_t b) {
     uint32_t d;
@@ -476,29 +501,26 @@ __device__ __forceinline__ void refill(Lane& l, Feed& f, const void* lds0, Mask 
     f.ring_b = nb < wrapped ? nb : wrapped;   // (nb mod ring size), as an unsigned min
 }
 
-// The refill check after a step pair (`carry` from dec_pair; lanes out of
-// range never carry, see lane_init).  A lane whose low window word is used
-// up (at most 32 unread bits) shifts and takes the next word.  After the
-// second-to-last step pair of the stream (final_check) it still shifts but
-// takes a word only below 24 unread bits (pos > 8 after the shift), since
-// the last pair reads at most 24.  There is no check after the last pair.
-__device__ __forceinline__ void check(Lane& l, Feed& f, const void* lds0, Mask carry,
-                                      bool final_check) {
-    if (final_check) {
-        refill(l, f, lds0, carry, carry & __ballot((l.q & 31u) > 8u));
-    } else {
-        refill(l, f, lds0, carry, carry);
-    }
+// The refill check after a segment of steps (`carry` from dec_pair or
+// dec_triple; lanes out of range never carry, see lane_init): a lane whose
+// low window word is used up (at most 32 unread bits) shifts and takes the
+// next word.  There is no check after a stream's last segment, and in the
+// last tile the checks go through check_last.
+__device__ __forceinline__ void check(Lane& l, Feed& f, const void* lds0, Mask carry) {
+    refill(l, f, lds0, carry, carry);
 }
 
 // check() in the last tile, with its kind chosen at run time (wave-uniform
-// flags selecting lane masks): none after the stream's last step pair, the
-// final check after the second-to-last one.
+// flags selecting lane masks): none after the stream's last segment; after
+// the second-to-last one (final_check) a lane still shifts but takes a
+// word only when it holds fewer bits than the last segment can read, that
+// is when pos > fin_pos after the shift (fin_pos = 32 - that many bits:
+// 8 for the pair schedule's 24).
 __device__ __forceinline__ void check_last(Lane& l, Feed& f, const void* lds0, Mask carry,
-                                           bool final_check, bool none) {
-    const Mask below24 = __ballot((l.q & 31u) > 8u);
+                                           bool final_check, bool none, uint32_t fin_pos) {
+    const Mask short_of_last = __ballot((l.q & 31u) > fin_pos);
     const Mask shift = none ? Mask(0) : carry;
-    refill(l, f, lds0, shift, final_check ? shift & below24 : shift);
+    refill(l, f, lds0, shift, final_check ? shift & short_of_last : shift);
 }
 
 // Start a chain (after feed_commit): every lane in range takes two words,
@@ -543,9 +565,10 @@ __device__ __forceinline__ void compose8(uint32_t ex_lo, uint32_t ex_hi, uint32_
 // The decode table is copied into LDS by the kDecBlock threads of a
 // decoder workgroup in two halves: table_fetch issues every load of the
 // thread, table_store writes them once they arrive.  Entries that would
-// step outside the table (nb > log2L or base + 2^nb > 2L) are replaced by a
-// harmless one, so a malformed table gives wrong bytes, never an
-// out-of-range LDS access.
+// step outside the table (nb > log2L or base + 2^nb > 2L), or read more
+// bits than the refill schedule allows (nb > 10 in a 2^11-state table), are
+// replaced by a harmless one, so a malformed table gives wrong bytes, never
+// an out-of-range LDS access.
 template <uint32_t L>
 struct TableRegs {
     static_assert(L % kDecBlock == 0, "the table is split evenly over the workgroup");
@@ -561,12 +584,14 @@ __device__ __forceinline__ void table_fetch(TableRegs<L>& r, const v2u* __restri
 template <uint32_t L>
 __device__ __forceinline__ void table_store(v2u* lds, const TableRegs<L>& r) {
     constexpr uint32_t log2L = 31 - __builtin_clz(L);
+    constexpr uint32_t max_nb =
+        log2L == tans_sched::kTripleLog2L ? tans_sched::kTripleMaxNb : log2L;
     #pragma unroll
     for (uint32_t k = 0; k < L / kDecBlock; k++) {
         v2u e = r.e[k];
         const uint32_t nb = e.x & 0xFFu;
         const uint32_t base = e.y >> 3;
-        if (nb > log2L || (e.x >> 27) != nb || (e.y & 7u) || base + (1u << nb) > L)
+        if (nb > max_nb || (e.x >> 27) != nb || (e.y & 7u) || base + (1u << nb) > L)
             e = v2u{e.x & 0x07FFFF00u, 0u};
         lds[threadIdx.x + k * kDecBlock] = e;
     }
@@ -576,7 +601,29 @@ template <int SPS>
 struct Alpha {
     static constexpr uint32_t L = SPS == 2 ? (1u << TANS_PAIR_LOG2L) : (1u << TANS_NIBBLE_LOG2L);
     static constexpr int kStagesPerTile = SPS == 2 ? 1 : 2;   // a stage is 8 steps
+    // refill schedule (schedule.h): segments of 2 steps, or 3, 3, 2 per stage
+    static constexpr bool kTriple = SPS == 1;
+    static_assert(kTriple == ((31 - __builtin_clz(L)) == tans_sched::kTripleLog2L),
+                  "the nibble alphabet's tables are the 3-3-2 schedule's");
+    static constexpr int kSegsPerStage = kTriple ? 3 : 4;
+    static constexpr int kSegsPerTile = kSegsPerStage * kStagesPerTile;
+    static constexpr int seg_first(int q) { return kTriple ? 3 * q : 2 * q; }
+    static constexpr int seg_len(int q) { return kTriple ? (q == 2 ? 2 : 3) : 2; }
+    // the final check's fin_pos when the stream ends with a whole tile
+    static constexpr uint32_t kFinPosFullTile =
+        32u - (uint32_t)(kTriple ? tans_sched::kTripleMaxNb * 2 : tans_sched::kPairFinalBelow);
 };
+
+// Segments of S steps in the last tile and the final check's fin_pos
+// (check_last), for a stream of n_tiles tiles.
+template <int SPS>
+__device__ __forceinline__ void last_tile_sched(int64_t S, int n_tiles, int& last_segs,
+                                                uint32_t& fin_pos) {
+    constexpr bool tri = Alpha<SPS>::kTriple;
+    last_segs = (int)(tans_sched::segments(S, tri) -
+                      (int64_t)(n_tiles - 1) * Alpha<SPS>::kSegsPerTile);
+    fin_pos = S > 0 ? 32u - (uint32_t)tans_sched::final_below(S, tri) : 0u;
+}
 
 // LDS of a decoder workgroup.  The table comes first so that its entries'
 // byte offsets are their LDS addresses.
@@ -628,42 +675,50 @@ struct Chains {
 };
 
 // Decode the 16 elements of one tile of every chain into exponent words
-// ex[c][4] (4 elements each).  q's scratch bits are cleared first (a step
-// pair adds less than 2^24 there).  LAST: the tile holds each stream's
-// final step pairs, last_pairs of them (the rest of the tile decodes past
-// the end: no checks there, so it reads only the lane's own window and the
-// table, and its bytes are discarded).
+// ex[c][4] (4 elements each).  q's scratch bits are cleared first (a
+// segment adds less than 2^24 there).  LAST: the tile holds each stream's
+// final segments, last_segs of them (the rest of the tile decodes past the
+// end: no checks there, so it reads only the lane's own window and the
+// table, and its bytes are discarded); fin_pos sets the final check
+// (check_last).
 template <int SPS, int C, bool LAST>
 __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ tbl, int lane,
                                          uint32_t (&ex)[C][4],
-                                         int last_pairs = 4 * Alpha<SPS>::kStagesPerTile) {
+                                         int last_segs = Alpha<SPS>::kSegsPerTile,
+                                         uint32_t fin_pos = Alpha<SPS>::kFinPosFullTile) {
+    using A = Alpha<SPS>;
     #pragma unroll
     for (int c = 0; c < C; c++) ch.l[c].q &= 0xF800001Fu;
-    static_for<0, Alpha<SPS>::kStagesPerTile>([&](auto H) {
+    static_for<0, A::kStagesPerTile>([&](auto H) {
         constexpr int h = decltype(H)::value;
         #pragma unroll
         for (int c = 0; c < C; c++) feed_stage(ch.f[c], ch.p[c], lane);
         uint32_t e[C][8];
-        #pragma unroll
-        for (int q = 0; q < kChecksPerStage; q++) {
+        static_for<0, A::kSegsPerStage>([&](auto Q) {
+            constexpr int q = decltype(Q)::value;
+            constexpr int i0 = A::seg_first(q);
             Mask carry[C];
             #pragma unroll
-            for (int c = 0; c < C; c++)
-                carry[c] = dec_pair(ch.l[c], tbl, e[c][2 * q], e[c][2 * q + 1]);
+            for (int c = 0; c < C; c++) {
+                if constexpr (A::seg_len(q) == 3)
+                    carry[c] = dec_triple(ch.l[c], tbl, e[c][i0], e[c][i0 + 1], e[c][i0 + 2]);
+                else
+                    carry[c] = dec_pair(ch.l[c], tbl, e[c][i0], e[c][i0 + 1]);
+            }
             if (LAST) {
-                // the step pair's index in the tile: pairs from last_pairs - 1
+                // the segment's index in the tile: segments from last_segs - 1
                 // on end the streams (no check) and the one before them gets
                 // the final check; selected on the masks, without branches
-                const int idx = h * kChecksPerStage + q;
+                const int idx = h * A::kSegsPerStage + q;
                 #pragma unroll
                 for (int c = 0; c < C; c++)
-                    check_last(ch.l[c], ch.f[c], tbl, carry[c], idx == last_pairs - 2,
-                               idx >= last_pairs - 1);
+                    check_last(ch.l[c], ch.f[c], tbl, carry[c], idx == last_segs - 2,
+                               idx >= last_segs - 1, fin_pos);
             } else {
                 #pragma unroll
-                for (int c = 0; c < C; c++) check(ch.l[c], ch.f[c], tbl, carry[c], false);
+                for (int c = 0; c < C; c++) check(ch.l[c], ch.f[c], tbl, carry[c]);
             }
-        }
+        });
         #pragma unroll
         for (int c = 0; c < C; c++) {
             if constexpr (SPS == 2) {
@@ -918,7 +973,8 @@ struct DecodeWave {
     int base;               // tiles this wave finished in earlier groups (pacing)
     bool full;              // both groups have 64 lanes in range (wave-uniform)
     bool lines;             // K % 16 == 0: rows start 16-byte aligned
-    int last_pairs;         // step pairs of the streams in the last tile
+    int last_segs;          // refill segments of the streams in the last tile
+    uint32_t fin_pos;       // the final check's threshold (check_last)
 
     // Tile t (P = t mod kSmAhead) holding n elements per lane (n < 16 only
     // for a ragged last tile); LAST: t is the last tile.
@@ -928,7 +984,7 @@ struct DecodeWave {
         // symbol come after every real one (no refill checks there), stay
         // inside the table, and their bytes are not stored.
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, last_pairs);
+        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, last_segs, fin_pos);
         pace(progress, lane, (uint32_t)(base + t), live);
         uint32_t w[C][4];
         #pragma unroll
@@ -1050,12 +1106,7 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     w.K = K;
     const int rag = (int)(N % kTile);
     w.n_tiles = (int)(N / kTile) + (rag ? 1 : 0);
-    {
-        // step pairs per lane, and those of the last tile
-        constexpr int kPairsPerTile = kTile / SPS / 2;
-        const int64_t pairs = (N / SPS + 1) / 2;
-        w.last_pairs = (int)(pairs - (int64_t)(w.n_tiles - 1) * kPairsPerTile);
-    }
+    last_tile_sched<SPS>(N / SPS, w.n_tiles, w.last_segs, w.fin_pos);
     w.tbl = tbl;
     w.sm_stride = K * 8;
     w.qoff = (uint32_t)(lane & 3) * (uint32_t)K + (uint32_t)(lane >> 2) * 4u;
@@ -1188,7 +1239,8 @@ struct GemmWave {
     uint32_t live;
     int64_t sm_stride;
     int n_tiles;
-    int last_pairs;         // step pairs of the streams in the last tile
+    int last_segs;          // refill segments of the streams in the last tile
+    uint32_t fin_pos;       // the final check's threshold (check_last)
     int lane;
     int q;                  // lane / 16: the lane's column chunk
     v4f acc[C];
@@ -1199,7 +1251,7 @@ struct GemmWave {
         // and its bytes past n are zeroed; every lane of a group is in range
         // (rows are padded to 64)
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, last_pairs);
+        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, last_segs, fin_pos);
         pace(progress, lane, (uint32_t)t, live);
         // x of the lane's columns: 64 t + 16 q (+ 8 for the second k-block),
         // or 64 t + 8 q in a half tile
@@ -1295,11 +1347,7 @@ __global__ __launch_bounds__(kDecBlock) void gemm_fused_kernel(
     const int per_lane = Nc / 4;                              // elements per lane (8 | per_lane)
     const int rag = per_lane % kTile;                         // 0 or 8
     w.n_tiles = per_lane / kTile + (rag ? 1 : 0);
-    {
-        constexpr int kPairsPerTile = kTile / SPS / 2;
-        const int pairs = (per_lane / SPS + 1) / 2;
-        w.last_pairs = pairs - (w.n_tiles - 1) * kPairsPerTile;
-    }
+    last_tile_sched<SPS>(per_lane / SPS, w.n_tiles, w.last_segs, w.fin_pos);
     w.sm_bytes = kLanes * 8u;
     Seg first[CH][kSlots];
     uint16_t st0[CH];

@@ -1,0 +1,63 @@
+// Refill schedule of a lane's decode steps, shared by the CPU encoder
+// (codec.cpp), the GPU encoder (encode.hip) and the decoders (kernels.hip).
+//
+// A lane's S decode steps are cut into segments.  A decoder reads each
+// segment's bits from one 32-bit window taken at the lane's bit position,
+// and after every segment but the last it checks the refill: a lane holding
+// at most 32 unread bits takes the next word of its group's stream (after
+// the second-to-last segment: only a lane holding fewer than `final_below`
+// bits, the most the last segment can read).  Every lane starts with two
+// words, so a lane enters each segment with at least 33 unread bits.
+//
+// * Tables of 2^12 states (the pair alphabet, nb <= 12): segments of two
+//   steps (at most 24 bits).
+// * Tables of 2^11 states (the nibble alphabet): every present symbol has a
+//   frequency of at least 2, so nb <= 10, and each 8 steps are cut into
+//   segments of 3, 3 and 2 steps (at most 30 bits).  Three steps per window
+//   and per check, against two, take 6 fewer VALU instructions per 8 steps.
+#ifndef TANS_SCHEDULE_H
+#define TANS_SCHEDULE_H
+
+#include <stdint.h>
+
+#ifdef __HIPCC__
+#define TANS_SCHED_FN __host__ __device__ __forceinline__
+#else
+#define TANS_SCHED_FN inline
+#endif
+
+namespace tans_sched {
+
+constexpr int kTripleLog2L = 11;    // tables of this size use 3-3-2 segments
+constexpr uint32_t kTripleMinFreq = 2;   // ... and every present symbol needs f >= 2
+constexpr uint32_t kTripleMaxNb = 10;
+constexpr int kAtMost = 32;         // a lane holding at most this many bits takes a word
+constexpr int kPairFinalBelow = 24; // pair schedule: the final check's threshold
+
+// Segments of S steps.
+TANS_SCHED_FN int64_t segments(int64_t S, bool triple) {
+    if (!triple) return (S + 1) / 2;
+    const int64_t r = S % 8;
+    return 3 * (S / 8) + (r == 0 ? 0 : r <= 3 ? 1 : r <= 6 ? 2 : 3);
+}
+
+// First step of segment j.
+TANS_SCHED_FN int64_t seg_start(int64_t j, bool triple) {
+    if (!triple) return 2 * j;
+    const int64_t w = j % 3;
+    return 8 * (j / 3) + (w == 0 ? 0 : w == 1 ? 3 : 6);
+}
+
+// Steps in the last segment of S > 0 steps.
+TANS_SCHED_FN int last_len(int64_t S, bool triple) {
+    return (int)(S - seg_start(segments(S, triple) - 1, triple));
+}
+
+// The final check's threshold: the most bits the last segment can read.
+TANS_SCHED_FN int final_below(int64_t S, bool triple) {
+    return triple ? (int)kTripleMaxNb * last_len(S, triple) : kPairFinalBelow;
+}
+
+}  // namespace tans_sched
+
+#endif  // TANS_SCHEDULE_H

@@ -13,9 +13,13 @@ the metadata key ``tans:name`` with a JSON description:
   for a TansMatrix (the layout of fp8_gemm_fused_tans).
 
 Plain tensors (scales, unencoded weights) are stored under their own names;
-``tans_format`` in the metadata names the layout version: v2 streams follow
-the carry-driven refill schedule and matrices the 16-row matrix-core lane
-groups (include/tans_amd.h); files of other versions are refused.
+``tans_format`` in the metadata names the layout version: v3 streams follow
+the carry-driven refill schedule (segments of two steps for the pair
+alphabet; 3, 3 and 2 steps for the nibble alphabet, whose tables give every
+present symbol a frequency of at least 2) and matrices the 16-row
+matrix-core lane groups (include/tans_amd.h).  v2 files are read when all
+their entries use the pair alphabet (its layout is unchanged); files of
+other versions, and v2 files with nibble entries, are refused.
 """
 from __future__ import annotations
 
@@ -25,7 +29,8 @@ import torch
 
 from .tans_codec import TansMatrix, TansTensor
 
-FORMAT = "tans-wave64-v2"
+FORMAT = "tans-wave64-v3"
+_PAIR_ONLY = "tans-wave64-v2"   # the pair layout is unchanged since this version
 _PARTS = ("comp", "states", "offsets", "sm", "freqs", "spread")
 
 
@@ -72,11 +77,16 @@ def load(path: str, device="cpu") -> dict:
     out: dict = {}
     with safe_open(path, framework="pt", device="cpu") as f:
         meta = f.metadata() or {}
-        if meta.get("tans_format") != FORMAT:
-            raise ValueError(f"{path}: not a {FORMAT} container (format "
-                             f"{meta.get('tans_format')!r}); re-encode it with this version")
+        fmt = meta.get("tans_format")
+        if fmt not in (FORMAT, _PAIR_ONLY):
+            raise ValueError(f"{path}: not a {FORMAT} container (format {fmt!r}); "
+                             "re-encode it with this version")
         keys = set(f.keys())
         encoded = {k[len("tans:"):]: json.loads(v) for k, v in meta.items() if k.startswith("tans:")}
+        if fmt == _PAIR_ONLY and any(d.get("alphabet") != "pair" for d in encoded.values()):
+            raise ValueError(f"{path}: {fmt} container with nibble-alphabet entries, whose "
+                             "streams follow the previous refill schedule; re-encode it with "
+                             "this version")
         for name, desc in encoded.items():
             parts = {p: f.get_tensor(f"{name}.{p}").to(device) for p in _PARTS}
             keys -= {f"{name}.{p}" for p in _PARTS}

@@ -122,8 +122,32 @@ def split_fp8(fp8_bytes: torch.Tensor, alphabet: str = "pair"):
     return symbols, sm
 
 
+# Every present symbol of a 2^11-state (nibble) table needs a frequency of
+# at least 2: then no step reads more than 10 bits, and the decoders read
+# three steps from one 32-bit window (the refill schedule of
+# csrc/schedule.h).
+NIBBLE_MIN_FREQ = 2
+
+
+def floor_freqs(freqs, fmin: int) -> np.ndarray:
+    """Raise every present symbol's frequency to at least ``fmin``, taking
+    the units from the largest frequencies (one at a time, the largest
+    first, lowest index on ties); the total is unchanged."""
+    f = np.asarray(freqs, dtype=np.int64).reshape(-1).copy()
+    low = (f > 0) & (f < fmin)
+    need = int((fmin - f[low]).sum())
+    f[low] = fmin
+    for _ in range(need):
+        i = int(np.argmax(f))
+        if f[i] <= fmin:
+            raise ValueError("floor_freqs: too many symbols for the table size")
+        f[i] -= 1
+    return f.astype(np.int32)
+
+
 def symbol_freqs(exp_freqs, alphabet: str = "pair") -> np.ndarray:
-    """Quantised symbol frequencies from a 16-entry exponent histogram."""
+    """Quantised symbol frequencies from a 16-entry exponent histogram
+    (the nibble alphabet's floored at NIBBLE_MIN_FREQ)."""
     nsym, n_states, _ = ALPHABETS[alphabet]
     # normalised in float32, as the reference does (tans_codec.py:126-128),
     # so the quantised frequencies match its pair_freqs
@@ -133,7 +157,8 @@ def symbol_freqs(exp_freqs, alphabet: str = "pair") -> np.ndarray:
     p = p / p.sum()
     if nsym == 256:
         p = (p[:, None] * p[None, :]).reshape(-1)
-    return quantize_freqs(p, target=n_states)
+        return quantize_freqs(p, target=n_states)
+    return floor_freqs(quantize_freqs(p, target=n_states), NIBBLE_MIN_FREQ)
 
 
 def _check_tile(tile: int, N: int) -> None:

@@ -86,6 +86,26 @@ def test_host_table_builder_rejects_inconsistent_input():
         T.build_decode_table(bad, f)                # symbol out of range
 
 
+def test_nibble_tables_need_frequencies_of_two():
+    """2^11-state tables are decoded three steps per 32-bit window, so every
+    present symbol needs f >= 2 (nb <= 10): the host table builders and the
+    CPU encoder reject a frequency of 1; symbol_freqs floors it."""
+    import numpy as np
+    from rans_vectoradd import _C, tans_codec as T
+    f = np.full(16, 128, dtype=np.int32)
+    f[0], f[1] = 1, 255                             # sums to 2048, one symbol at 1
+    sp = T.build_spread(f)
+    with pytest.raises(RuntimeError, match=">= 2"):
+        T.build_decode_table(sp, f)
+    sym = torch.zeros((64, 16), dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match=">= 2"):
+        _C.tans_encode_interleaved(sym, torch.from_numpy(f), torch.from_numpy(sp))
+    hist = np.full(16, 1000.0)
+    hist[0] = 0.1                                    # far below 1/2048: quantized to 1
+    g = T.symbol_freqs(hist, "nibble")
+    assert g.sum() == 2048 and g.min() >= 2
+
+
 def test_gemm_and_gpu_encode_entry_points_validate_before_launch():
     """The decode-GEMM, raw GEMM and GPU encoder entry points reject bad
     shapes and sizes with TANS_EINVAL before touching the device."""

@@ -62,8 +62,27 @@ def test_symbol_freqs_and_spread_match_oracle(T, alphabet):
     p = p / p.sum()
     if alphabet == "pair":
         p = (p[:, None] * p[None, :]).reshape(-1)
-    assert np.array_equal(f, O.quantize_freqs(p, L))
+    q = O.quantize_freqs(p, L).astype(np.int64)
+    if alphabet == "nibble":
+        # the floor of the 3-3-2 refill schedule: the two frequency-1
+        # exponents go to 2, and the two units come off the largest (556)
+        assert sorted(np.flatnonzero(q == 1).tolist()) == [0, 1]
+        q[q == 1] = 2
+        q[int(np.argmax(q))] -= 2
+    assert np.array_equal(f, q)
     assert np.array_equal(T.build_spread(f), O.build_spread(f, L))
+
+
+def test_floor_freqs(T):
+    """Present symbols below the floor are raised to it; the units come off
+    the largest frequencies one at a time (lowest index on ties), absent
+    symbols stay absent, and the total is kept."""
+    assert T.floor_freqs([1, 1, 5, 5], 2).tolist() == [2, 2, 4, 4]
+    assert T.floor_freqs([0, 1, 7, 8], 2).tolist() == [0, 2, 7, 7]
+    assert T.floor_freqs([3, 0, 2, 11], 2).tolist() == [3, 0, 2, 11]
+    assert T.floor_freqs([1, 1, 1, 13], 4).tolist() == [4, 4, 4, 4]
+    with pytest.raises(ValueError):
+        T.floor_freqs([1, 1, 1, 1], 2)
 
 
 def test_absent_exponent_gives_valid_pair_table(T):

@@ -76,11 +76,35 @@ def test_container_rejects_other_files(tmp_path):
         container.load(path)
     with pytest.raises(ValueError):
         container.save(path, {"x": torch.zeros(2)}, metadata={"tans_format": "y"})
-    # a file of the previous layout version (other stream schedule and matrix lanes)
+    # a file of an older layout version (other stream schedule and matrix lanes)
     old = os.path.join(tmp_path, "v1.safetensors")
     save_file({"x": torch.zeros(2)}, old, metadata={"tans_format": "tans-wave64-v1"})
     with pytest.raises(ValueError, match="re-encode"):
         container.load(old)
+
+
+def test_container_reads_v2_pair_entries_only(tmp_path):
+    """v2 containers differ from v3 only in the nibble alphabet's refill
+    schedule: their pair entries load, a nibble entry is refused."""
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+    from rans_vectoradd import container, data as D, tans_codec as T
+    q, _ = D.gaussian_fp8_bytes(64 * 32, seed=3)
+    for alphabet, ok in (("pair", True), ("nibble", False)):
+        t = T.TansTensor.from_tuple(T.encode(q.reshape(64, 32), D.exp_histogram(q),
+                                             alphabet=alphabet), 64, 32, alphabet)
+        path = os.path.join(tmp_path, f"{alphabet}.safetensors")
+        container.save(path, {"w": t})
+        with safe_open(path, framework="pt") as f:
+            meta, tensors = f.metadata(), {k: f.get_tensor(k) for k in f.keys()}
+        meta["tans_format"] = "tans-wave64-v2"
+        v2 = os.path.join(tmp_path, f"{alphabet}_v2.safetensors")
+        save_file(tensors, v2, metadata=meta)
+        if ok:
+            assert torch.equal(container.load(v2)["w"].comp, t.comp)
+        else:
+            with pytest.raises(ValueError, match="re-encode"):
+                container.load(v2)
 
 
 def _checkpoint(path):

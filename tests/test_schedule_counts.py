@@ -1,63 +1,98 @@
 """The refill schedule's word count in closed form.
 
 csrc/encode.hip counts the stream words each lane takes from two bit totals
-(up to the third- and second-to-last step pairs) instead of replaying the
+(up to the third- and second-to-last segments) instead of replaying the
 schedule.  This checks that closed form against a step-by-step replay of the
-decoders' rule (two words to start; after every step pair but the last, take
-a word at <= 32 unread bits; after the second-to-last, below 24) on random
-bit counts, including zero-bit steps, odd step counts and the largest step
-(12 bits, pair alphabet).  The GPU encoder's output is checked byte for byte
-against the CPU encoder in tests/test_gpu_encode.py.
+decoders' rule on random bit counts, including zero-bit steps, step counts
+that end inside a segment, and the largest steps.  The rule: two words to
+start; the steps are cut into segments (step pairs with 2^12-state tables,
+nb <= 12; 3, 3 and 2 steps of every 8 with 2^11-state tables, nb <= 10);
+after every segment but the last a lane takes a word at <= 32 unread bits,
+after the second-to-last only below what the last segment can read (24 for
+pairs, 10 per step of the last segment otherwise).  The GPU encoder's
+output is checked byte for byte against the CPU encoder in
+tests/test_gpu_encode.py.
 """
 import random
 
+import pytest
 
-def replay(nbs):
+
+def segments(S, triple):
+    """(first, end) steps of each segment of S steps."""
+    out, i = [], 0
+    lens = (3, 3, 2) if triple else (2,)
+    while i < S:
+        for n in lens:
+            if i >= S:
+                break
+            out.append((i, min(i + n, S)))
+            i += n
+    return out
+
+
+def final_below(segs, triple):
+    a, b = segs[-1]
+    return 10 * (b - a) if triple else 24
+
+
+def replay(nbs, triple):
     """Words taken by one lane whose steps consume nbs[0], nbs[1], ... bits."""
-    S = len(nbs)
-    if S == 0:
+    segs = segments(len(nbs), triple)
+    if not segs:
         return 0
-    n_pairs = (S + 1) // 2
     taken, held = 2, 64
-    for q in range(n_pairs):
-        held -= sum(nbs[2 * q:2 * q + 2])
+    for q, (a, b) in enumerate(segs):
+        seg_bits = sum(nbs[a:b])
+        assert seg_bits <= 30 if triple else seg_bits <= 24
+        assert held >= 33 or q + 1 == len(segs) or q == 0, "at least 33 bits into a segment"
+        held -= seg_bits
         assert held >= 0, "the schedule never lets a lane run dry"
-        if q + 1 < n_pairs:
-            below = 24 if q + 2 == n_pairs else 33
+        if q + 1 < len(segs):
+            below = final_below(segs, triple) if q + 2 == len(segs) else 33
             if held < below:
                 taken += 1
                 held += 32
     return taken
 
 
-def closed_form(nbs):
-    """The encoder's count: t = c3 // 32 + 2, plus one when 32 t - c2 < 24."""
-    S = len(nbs)
-    if S == 0:
+def closed_form(nbs, triple):
+    """The encoder's count: t = c3 // 32 + 2, plus one when 32 t - c2 is
+    below the final threshold."""
+    segs = segments(len(nbs), triple)
+    n = len(segs)
+    if n == 0:
         return 0
-    n = (S + 1) // 2
     if n == 1:
         return 2
     bits = sum(nbs)
-    b1 = sum(nbs[2 * (n - 1):])          # the last pair
-    b2 = sum(nbs[2 * (n - 2):])          # the last two pairs
+    b1 = sum(nbs[segs[-1][0]:])          # the last segment
+    b2 = sum(nbs[segs[-2][0]:])          # the last two segments
     c2 = bits - b1
     c3 = bits - b2 if n >= 3 else 0
     t = c3 // 32 + 2
-    return t + (1 if 32 * t - c2 < 24 else 0)
+    return t + (1 if 32 * t - c2 < final_below(segs, triple) else 0)
 
 
-def test_closed_form_equals_replay():
+@pytest.mark.parametrize("triple,top_nb", [(False, 12), (True, 10)])
+def test_closed_form_equals_replay(triple, top_nb):
     rng = random.Random(7)
     for _ in range(20000):
-        S = rng.choice([0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 16, 31, 64, 257])
-        top = rng.choice([0, 1, 2, 5, 11, 12])
+        S = rng.choice([0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 16, 31, 64, 257])
+        top = rng.choice([0, 1, 2, 5, top_nb - 1, top_nb])
         nbs = [rng.randint(0, top) if rng.random() < 0.8 else top for _ in range(S)]
-        assert closed_form(nbs) == replay(nbs), nbs
+        assert closed_form(nbs, triple) == replay(nbs, triple), nbs
 
 
-def test_closed_form_extremes():
+@pytest.mark.parametrize("triple,top_nb", [(False, 12), (True, 10)])
+def test_closed_form_extremes(triple, top_nb):
     for S in range(0, 40):
-        for v in (0, 1, 11, 12):
+        for v in (0, 1, top_nb - 1, top_nb):
             nbs = [v] * S
-            assert closed_form(nbs) == replay(nbs), (S, v)
+            assert closed_form(nbs, triple) == replay(nbs, triple), (S, v)
+
+
+def test_segments_of_the_triple_schedule():
+    assert segments(8, True) == [(0, 3), (3, 6), (6, 8)]
+    assert segments(12, True) == [(0, 3), (3, 6), (6, 8), (8, 11), (11, 12)]
+    assert segments(5, False) == [(0, 2), (2, 4), (4, 5)]
