@@ -34,7 +34,10 @@
  *     32 unread bits takes the next stream word (lanes in ascending order)
  *     and gains 32 bits; after the second-to-last segment only a lane
  *     holding fewer bits than the last segment can read does (24 with
- *     2^12-state tables, 10 per step of the last segment with 2^11).
+ *     2^12-state tables, 10 per step of the last segment with 2^11),
+ *     except when the last 16-element tile holds the last segment alone
+ *     (N > 16 and N % 16 in 1..4 with 2^12-state tables, 1..3 with 2^11):
+ *     that check is then the plain one.
  *     Streams start on 16-byte boundaries; 1 KiB of zero words follows the
  *     last one.  offsets is int64 [n_groups + 1], in words.
  *   - states[k] is lane k's initial decoder state in [L, 2L).
@@ -139,11 +142,18 @@ int tans_fp8_vecadd_raw(const void* a, const void* b, void* c, int64_t n,
 int tans_stream_probe(int32_t mode, int32_t nontemporal, const void* a, const void* b,
                       void* c, int64_t n, void* sink, void* stream);
 
-/* Device decode table from device spread/freqs (no host round trip).
- * Same output as tans_build_decode_table.                               */
+/* Device decode table from device spread/freqs (no host round trip):
+ * the build of rans_vectoradd/tans_codec.py:63-87 and csrc/tans_decode.cu:23-59,
+ * same output as tans_build_decode_table.  The kernel checks what the host
+ * builder checks (frequencies summing to 2^log2L, every present symbol of a
+ * 2^11-state table at frequency >= 2, spread symbols in the alphabet, slot
+ * counts equal to frequencies) and, on a failure, sets *status (a device
+ * int, may be NULL; the caller zeroes it) to TANS_ETABLE, in stream order.
+ * A failed table still decodes without out-of-range accesses, to wrong
+ * bytes.                                                                */
 int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs,
                                    int32_t nsym, int32_t log2L, uint32_t* table,
-                                   void* stream);
+                                   int32_t* status, void* stream);
 
 /* Fused decode of two encodings (same table) + FP8 add.
  * out is tiled [N/16, K, 16]: out[(t*K + k)*16 + i] = element 16t+i of

@@ -378,7 +378,9 @@ int ora_ref_decode_add(const uint8_t* a_comp8, const int32_t* a_off, const uint1
  *   cut into segments, and after each segment except the last, each active
  *   lane (ascending j) holding at most 32 unread bits takes the next stream
  *   word (+32 bits); after the second-to-last segment only a lane holding
- *   fewer bits than the last segment can read does.  Segments: with
+ *   fewer bits than the last segment can read does, unless the last tile of
+ *   16 elements (16/sps steps) holds that last segment alone: then that
+ *   check is the plain one.  Segments: with
  *   2^11-state tables (whose symbols all have f >= 2, so nb <= 10), every 8
  *   steps are cut into 3, 3 and 2 steps, and the last segment can read
  *   10 bits per step; with other tables, step pairs (2p, 2p+1), and the
@@ -486,7 +488,10 @@ int ora_w64_decode(const uint8_t* comp8, const int64_t* offsets, const uint16_t*
         const int64_t n_seg = steps > 0 ? SEG_OF(steps - 1) + 1 : 0;
         int64_t last_start = steps - 1;       /* first step of the last segment */
         while (last_start > 0 && SEG_OF(last_start - 1) == n_seg - 1) last_start--;
-        const uint64_t final_below = triple ? (uint64_t)(10 * (steps - last_start)) : 24;
+        /* a last 16-element tile of one segment makes the final check the plain one */
+        const int64_t tile_steps = 16 / sps;
+        const int one_seg_tile = steps > tile_steps && last_start == tile_steps * ((steps - 1) / tile_steps);
+        const uint64_t final_below = one_seg_tile ? 33 : triple ? (uint64_t)(10 * (steps - last_start)) : 24;
         for (int64_t i = 0; i < steps && !bad; i++) {
             for (int j = 0; j < lanes && !bad; j++) {
                 int64_t k = g * 64 + j;

@@ -138,6 +138,15 @@ const char* tans_last_error(void) { return g_err.c_str(); }
 
 void tans_internal_set_error(const char* msg) { g_err = msg ? msg : ""; }
 
+// The refill thresholds after segment j of a stream of S steps (schedule.h):
+// the one the encoders apply (which = 0) and the one the GPU decoders'
+// placement of checks amounts to (which = 1); 0 = no check.  Not part of the
+// public ABI: the CPU tests compare the two.
+int tans_internal_check_below(int32_t which, int64_t S, int32_t triple, int64_t j) {
+    return which ? tans_sched::decoder_below(S, triple != 0, j)
+                 : tans_sched::encoder_below(S, triple != 0, j);
+}
+
 int tans_split_fp8(const uint8_t* fp8, int64_t K, int64_t N, int32_t sps,
                    uint8_t* symbols, uint8_t* sm) {
     if ((!fp8 && K * N != 0) || K < 0 || N < 0 || (N % 2) != 0)
@@ -274,8 +283,7 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
             const bool triple = log2L == tans_sched::kTripleLog2L;
             const int64_t n_seg = tans_sched::segments(S, triple);
             for (int64_t q = 0; q + 1 < n_seg; q++) {
-                const int32_t below = (q + 2 == n_seg) ? tans_sched::final_below(S, triple)
-                                                        : tans_sched::kAtMost + 1;
+                const int32_t below = tans_sched::encoder_below(S, triple, q);
                 const int64_t i0 = tans_sched::seg_start(q, triple);
                 const int64_t i1 = tans_sched::seg_start(q + 1, triple);
                 for (int j = 0; j < lanes; j++) {

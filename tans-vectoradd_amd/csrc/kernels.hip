@@ -185,15 +185,25 @@ __global__ __launch_bounds__(kBlock) void stream_probe_kernel(const v4u* __restr
 // own bit is 0); mbcnt of that mask is the place, its popcount the count,
 // and the last lane holding each symbol writes the count to LDS.  An exclusive prefix over segments (16
 // segments per thread, then 4 partial totals per symbol) gives the rest.
+//
+// The kernel checks what the host builder (codec.cpp) checks: frequencies
+// not negative and summing to L, every present symbol of a 2^11-state
+// table at a frequency of at least 2, spread symbols inside the alphabet
+// and each symbol's slot count equal to its frequency (a rank below it).
+// On any failure it sets *status (when given) to TANS_ETABLE; the table it
+// writes is then wrong but still in range: a symbol outside the alphabet is
+// folded into it, and the decoders' table_store replaces entries that
+// would step outside the table or read too many bits.
 // ---------------------------------------------------------------------
 constexpr int kTableWaves = 16;
 constexpr int kTableSegs = kTableWaves * 4;   // 64 segments of 64 slots at L = 4096
 
 __global__ __launch_bounds__(kTableWaves * 64) void table_kernel(
     const int32_t* __restrict__ spread, const int32_t* __restrict__ freqs, int nsym, int log2L,
-    v2u* __restrict__ table) {
+    v2u* __restrict__ table, int32_t* __restrict__ status) {
     __shared__ uint16_t cnt[kTableSegs][256];   // per segment: counts, then exclusive prefix
     __shared__ uint16_t tot[4][256];            // prefix totals of segment quarters
+    __shared__ uint32_t fsum, bad;              // sum of the frequencies; any check failed
     const uint32_t L = 1u << log2L;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -202,15 +212,24 @@ __global__ __launch_bounds__(kTableWaves * 64) void table_kernel(
     const int nseg = kTableWaves * rounds;
     for (uint32_t i = threadIdx.x; i < kTableSegs * 256 / 2; i += blockDim.x)
         reinterpret_cast<uint32_t*>(&cnt[0][0])[i] = 0u;
+    if (threadIdx.x == 0) { fsum = 0u; bad = 0u; }
     __syncthreads();
+    uint32_t my_bad = 0u;
+    if ((int)threadIdx.x < nsym) {
+        const int32_t f = freqs[threadIdx.x];
+        const int32_t min_f = log2L == tans_sched::kTripleLog2L ? (int32_t)tans_sched::kTripleMinFreq : 1;
+        if (f < 0 || f > (int32_t)L || (f > 0 && f < min_f)) my_bad = 1u;
+        else atomicAdd(&fsum, (uint32_t)f);
+    }
     uint32_t sym[4] = {0u, 0u, 0u, 0u}, rank[4] = {0u, 0u, 0u, 0u};
     #pragma unroll
     for (int r = 0; r < 4; r++) {
         if (r >= rounds) break;
         const int seg = wave * rounds + r;
-        // a symbol outside the alphabet is folded into it: a wrong table,
-        // never an out-of-range access (the host builder rejects such input)
-        const uint32_t sv = (uint32_t)spread[seg * 64 + lane] & (uint32_t)(nsym - 1);
+        // a symbol outside the alphabet is folded into it (and reported)
+        const int32_t raw = spread[seg * 64 + lane];
+        if (raw < 0 || raw >= nsym) my_bad = 1u;
+        const uint32_t sv = (uint32_t)raw & (uint32_t)(nsym - 1);
         sym[r] = sv;
         // the lanes holding the same symbol: for each symbol bit, the ballot
         // of lanes with that bit set, complemented where this lane's bit is 0
@@ -256,13 +275,19 @@ __global__ __launch_bounds__(kTableWaves * 64) void table_kernel(
         const uint32_t sv = sym[r];
         uint32_t before = 0;
         for (int qq = 0; qq < (seg >> 4); qq++) before += tot[qq][sv];
-        const uint32_t xp = (uint32_t)freqs[sv] + before + cnt[seg][sv] + rank[r];
+        const uint32_t f = (uint32_t)freqs[sv];
+        const uint32_t rk = before + cnt[seg][sv] + rank[r];   // rank among sv's slots
+        if (rk >= f) my_bad = 1u;                              // more slots than its frequency
+        const uint32_t xp = f + rk;
         const int top = xp ? 31 - __builtin_clz(xp) : log2L;
         const int nb = top < log2L ? log2L - top : 0;
         const uint32_t base = xp << nb;
         const uint32_t ex = (nsym == 256) ? (((sv >> 4) << 11) | ((sv & 0xFu) << 19)) : (sv << 11);
         table[seg * 64 + lane] = v2u{(uint32_t)nb | ex | ((uint32_t)nb << 27), (base - L) * 8u};
     }
+    if (my_bad) bad = 1u;   // benign race: every writer stores 1
+    __syncthreads();
+    if (threadIdx.x == 0 && status && (bad || fsum != L)) *status = TANS_ETABLE;
 }
 
 // ---------------------------------------------------------------------
@@ -615,7 +640,10 @@ struct Alpha {
 };
 
 // Segments of S steps in the last tile and the final check's fin_pos
-// (check_last), for a stream of n_tiles tiles.
+// (check_last), for a stream of n_tiles tiles.  When the last tile holds a
+// single segment, the final check follows the last segment of the tile
+// before, and the schedule makes it the plain check there (schedule.h), so
+// every tile but the last takes the plain path.
 template <int SPS>
 __device__ __forceinline__ void last_tile_sched(int64_t S, int n_tiles, int& last_segs,
                                                 uint32_t& fin_pos) {
@@ -712,8 +740,9 @@ __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ 
                 const int idx = h * A::kSegsPerStage + q;
                 #pragma unroll
                 for (int c = 0; c < C; c++)
-                    check_last(ch.l[c], ch.f[c], tbl, carry[c], idx == last_segs - 2,
-                               idx >= last_segs - 1, fin_pos);
+                    check_last(ch.l[c], ch.f[c], tbl, carry[c],
+                               tans_sched::end_is_final(last_segs, idx),
+                               tans_sched::end_is_none(last_segs, idx), fin_pos);
             } else {
                 #pragma unroll
                 for (int c = 0; c < C; c++) check(ch.l[c], ch.f[c], tbl, carry[c]);
@@ -1078,6 +1107,7 @@ struct DecodeWave {
         }
     }
 };
+
 
 template <int SPS>
 __global__ __launch_bounds__(kDecBlock) void decode_kernel(
@@ -1731,12 +1761,14 @@ int tans_stream_probe(int32_t mode, int32_t nontemporal, const void* a, const vo
 }
 
 int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs, int32_t nsym,
-                                   int32_t log2L, uint32_t* table, void* stream) {
+                                   int32_t log2L, uint32_t* table, int32_t* status,
+                                   void* stream) {
     if (!spread || !freqs || !table) return fail(TANS_EINVAL, "table: null pointer");
     if (!((nsym == 256 && log2L == TANS_PAIR_LOG2L) || (nsym == 16 && log2L == TANS_NIBBLE_LOG2L)))
         return fail(TANS_EINVAL, "table: need (nsym 256, log2L 12) or (nsym 16, log2L 11)");
+    if (status && !aligned(status, 4)) return fail(TANS_EINVAL, "table: status must be 4-byte aligned");
     hipLaunchKernelGGL(table_kernel, dim3(1), dim3(kTableWaves * 64), 0, (hipStream_t)stream, spread, freqs,
-                       (int)nsym, (int)log2L, (v2u*)table);
+                       (int)nsym, (int)log2L, (v2u*)table, status);
     return hip_check(hipGetLastError(), "table_kernel launch");
 }
 

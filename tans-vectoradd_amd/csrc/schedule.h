@@ -53,9 +53,50 @@ TANS_SCHED_FN int last_len(int64_t S, bool triple) {
     return (int)(S - seg_start(segments(S, triple) - 1, triple));
 }
 
+// Decode steps per 16-element tile (the sign/mantissa tile of the format):
+// 8 pair steps, or 16 steps of the 3-3-2 schedule (two of its 8-step
+// periods, so a tile boundary is always a segment boundary).
+TANS_SCHED_FN int64_t tile_steps(bool triple) { return triple ? 16 : 8; }
+
+// Segments in the last tile of a stream of S > 0 steps.
+TANS_SCHED_FN int64_t last_tile_segments(int64_t S, bool triple) {
+    const int64_t ts = tile_steps(triple);
+    return segments(S - ts * ((S - 1) / ts), triple);
+}
+
 // The final check's threshold: the most bits the last segment can read.
+// When the last tile holds a single segment, the final check follows the
+// last segment of the tile before it; it is then the plain check (a word
+// at kAtMost bits or fewer), so that the decoders run every tile but the
+// last through one code path.
 TANS_SCHED_FN int final_below(int64_t S, bool triple) {
+    if (S > tile_steps(triple) && last_tile_segments(S, triple) == 1) return kAtMost + 1;
     return triple ? (int)kTripleMaxNb * last_len(S, triple) : kPairFinalBelow;
+}
+
+// The encoders' threshold after segment j of S steps: a lane holding fewer
+// bits takes a word; 0 after the last segment (no check).
+TANS_SCHED_FN int encoder_below(int64_t S, bool triple, int64_t j) {
+    const int64_t n_seg = segments(S, triple);
+    return j + 1 >= n_seg ? 0 : j + 2 == n_seg ? final_below(S, triple) : kAtMost + 1;
+}
+
+// How the decoders place the checks.  Every tile but the last takes the
+// plain path (every check at kAtMost + 1); the last tile, starting with
+// `segs` segments, puts the final check after its segment segs - 2 and
+// none from segment segs - 1 on.
+TANS_SCHED_FN bool end_is_final(int segs, int idx) { return idx == segs - 2; }
+TANS_SCHED_FN bool end_is_none(int segs, int idx) { return idx >= segs - 1; }
+
+// The decoders' threshold after segment j, from that placement (equal to
+// encoder_below for every S and j).
+TANS_SCHED_FN int decoder_below(int64_t S, bool triple, int64_t j) {
+    const int64_t n_seg = segments(S, triple);
+    const int64_t first = n_seg - last_tile_segments(S, triple);   // the last tile's first segment
+    if (j < first) return kAtMost + 1;
+    const int segs = (int)(n_seg - first), idx = (int)(j - first);
+    return end_is_none(segs, idx) ? 0 : end_is_final(segs, idx) ? final_below(S, triple)
+                                                                 : kAtMost + 1;
 }
 
 }  // namespace tans_sched

@@ -118,6 +118,34 @@ def _sm_bytes(K: int, N: int) -> int:
     return ((N + TANS_TILE - 1) // TANS_TILE) * K * 8
 
 
+# (spread, freqs) pairs whose device table build reported no inconsistency:
+# id pair -> (weak references, data pointers and version counters).  A pair
+# is read back (one host synchronisation) only the first time it is seen and
+# after it changes in place.
+_VALID_TABLES: dict = {}
+_VALID_TABLES_MAX = 64
+
+
+def _table_key(spread: torch.Tensor, freqs: torch.Tensor):
+    return (spread.data_ptr(), spread._version, freqs.data_ptr(), freqs._version)
+
+
+def _table_known_valid(spread: torch.Tensor, freqs: torch.Tensor) -> bool:
+    hit = _VALID_TABLES.get((id(spread), id(freqs)))
+    if hit is None:
+        return False
+    ws, wf, key = hit
+    return ws() is spread and wf() is freqs and key == _table_key(spread, freqs)
+
+
+def _remember_valid_table(spread: torch.Tensor, freqs: torch.Tensor) -> None:
+    import weakref
+    if len(_VALID_TABLES) >= _VALID_TABLES_MAX:
+        _VALID_TABLES.clear()
+    _VALID_TABLES[(id(spread), id(freqs))] = (weakref.ref(spread), weakref.ref(freqs),
+                                              _table_key(spread, freqs))
+
+
 def gpu_tans_decode(compressed: torch.Tensor, offsets: torch.Tensor, states: torch.Tensor,
                     partial_cnts: torch.Tensor, sign_mantissa: torch.Tensor,
                     spread: torch.Tensor, freqs: torch.Tensor,
@@ -125,7 +153,12 @@ def gpu_tans_decode(compressed: torch.Tensor, offsets: torch.Tensor, states: tor
     """Standalone decode -> uint8 [n_fp8_per_stream, K].  (csrc/tans_decode.cu:159-210)
 
     The decode table is built on the device from spread/freqs, without the
-    reference's host round trip."""
+    reference's host round trip.  Like the reference's TORCH_CHECKs in its
+    table build (csrc/tans_decode.cu:38,50), an inconsistent spread/freqs
+    pair raises RuntimeError: the device build's status is read back the
+    first time a pair is used (and after it changes in place); later calls
+    with the same tensors, and calls under graph capture, do not wait on
+    the device."""
     _check_dev("compressed", compressed, torch.uint8)
     _check_dev("offsets", offsets, torch.int64)
     _check_dev("states", states, torch.uint16)
@@ -149,9 +182,21 @@ def gpu_tans_decode(compressed: torch.Tensor, offsets: torch.Tensor, states: tor
         return out
     with _on(dev):
         table = torch.empty(2 << log2L, dtype=torch.int32, device=dev)
+        verify = (not _table_known_valid(spread, freqs)
+                  and not torch.cuda.is_current_stream_capturing())
+        status = torch.zeros(1, dtype=torch.int32, device=dev) if verify else None
         stream = _stream(dev)
         check(lib.tans_build_decode_table_device(_ptr(spread), _ptr(freqs), nsym, log2L,
-                                                 _ptr(table), stream), "gpu_tans_decode")
+                                                 _ptr(table),
+                                                 _ptr(status) if verify else None, stream),
+              "gpu_tans_decode")
+        if verify:
+            rc = int(status.item())
+            _require(rc == 0, "gpu_tans_decode: spread and freqs do not form a valid decode "
+                              "table (frequencies must sum to the spread size, match the "
+                              "spread's symbol counts, and be >= 2 for every present symbol "
+                              "of a 2^11-state table)")
+            _remember_valid_table(spread, freqs)
         check(lib.tans_decode(_ptr(compressed), compressed.numel(), _ptr(offsets), _ptr(states),
                               _ptr(sign_mantissa), _ptr(table), log2L, K, N, _ptr(out), stream),
               "gpu_tans_decode")

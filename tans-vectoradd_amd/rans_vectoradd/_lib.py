@@ -63,7 +63,7 @@ for _name, _args in {
     "tans_fp8_memcpy": [_P, _P, _I64, _P],
     "tans_fp8_vecadd_raw": [_P, _P, _P, _I64, _P],
     "tans_stream_probe": [_I32, _I32, _P, _P, _P, _I64, _P, _P],
-    "tans_build_decode_table_device": [_P, _P, _I32, _I32, _P, _P],
+    "tans_build_decode_table_device": [_P, _P, _I32, _I32, _P, _P, _P],
     "tans_fp8_vecadd_fused": [_P, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I32,
                               _I64, _I64, _P, _P],
     "tans_decode": [_P, _I64, _P, _P, _P, _P, _I32, _I64, _I64, _P, _P],

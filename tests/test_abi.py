@@ -51,7 +51,7 @@ def test_gpu_entry_points_validate_before_launch():
                                      dummy, dummy, 12, 64, 16, dummy, None) == -1
     assert lib.tans_decode(dummy, 1024, dummy, dummy, dummy, dummy, 12, 64, 3, dummy, None) == -1
     assert lib.tans_decode(dummy, 1024, dummy, dummy, dummy, dummy, 12, 0, 16, dummy, None) == 0
-    assert lib.tans_build_decode_table_device(dummy, dummy, 16, 12, dummy, None) == -1
+    assert lib.tans_build_decode_table_device(dummy, dummy, 16, 12, dummy, None, None) == -1
     assert lib.tans_stream_probe(3, 1, dummy, dummy, dummy, 16, dummy, None) == -1
     assert b"mode" in lib.tans_last_error()
     assert lib.tans_stream_probe(2, 1, dummy, None, dummy, 16, None, None) == -1

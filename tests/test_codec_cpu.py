@@ -155,6 +155,24 @@ def test_encode_roundtrip_reference_test_cases(T, alphabet, K, N):
     assert sm.shape == ((N + 15) // 16, K, 8)
 
 
+@pytest.mark.parametrize("alphabet,N", [("pair", 18), ("pair", 20), ("pair", 36),
+                                         ("nibble", 18), ("nibble", 34), ("pair", 22),
+                                         ("nibble", 20)])
+def test_encode_roundtrip_last_tile_of_one_segment(T, alphabet, N):
+    """Streams whose last 16-element tile holds a single segment (pair: N %
+    16 = 2 or 4, nibble: N % 16 = 2), where the check after the
+    second-to-last segment is the plain one, and two neighbours where it is
+    the final one; uniformly random bytes with the (mismatched) Qwen3
+    table, so lanes end that segment holding every number of bits.  The
+    oracle's checker decodes the CPU encoder's streams, consuming every
+    word and bit."""
+    from rans_vectoradd import data as D
+    K = 2000
+    g = torch.Generator().manual_seed(N)
+    fp8 = torch.randint(0, 256, (K, N), dtype=torch.uint8, generator=g)
+    _encode_check(T, fp8, torch.tensor(D.QWEN3_14B_FP8_EXP), alphabet)
+
+
 def test_config0_cpu_roundtrip_bits_per_byte(T):
     """2^24 values N(0, 0.02) scaled to |max| = 448 and
     RNE-cast; 16-symbol alphabet, 2^11-state table from the data's own

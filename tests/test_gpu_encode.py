@@ -34,13 +34,17 @@ def _compare(T, fp8, hist, alphabet):
 @pytest.mark.parametrize("alphabet", ALPHABETS)
 @pytest.mark.parametrize("K,N", [(128, 128), (1024, 128), (10000, 128), (100000, 128),
                                  (64, 2), (65, 18), (200, 130), (3, 1000), (1, 16),
-                                 (127, 4096), (130, 30), (4096, 14), (300, 208), (70, 48)])
+                                 (127, 4096), (130, 30), (4096, 14), (300, 208), (70, 48),
+                                 (2000, 20), (2000, 36), (1000, 34)])
 def test_gpu_encode_matches_cpu(R, alphabet, K, N):
     """N % 16 == 0 takes the backward pass that reads rows in 128-byte blocks
     (whole blocks at N = 128, 4096; a partial last block at 208, 48, 16) and
     writes the sign/mantissa tiles itself; the other widths read one step's
     bytes at a time and leave the tiles to enc_sm_kernel.  K % 64 != 0 and
-    K < 64 give groups with lanes out of range; N = 2 (pair) is one step."""
+    K < 64 give groups with lanes out of range; N = 2 (pair) is one step.
+    N = 18, 20, 34, 36 end in a tile of one refill segment (18, 34 with both
+    alphabets, 20, 36 with pairs), where the check before it is the plain
+    one."""
     from rans_vectoradd import tans_codec as T
     _say(f"case: encode_gpu K={K} N={N} {alphabet}")
     torch.manual_seed(42)

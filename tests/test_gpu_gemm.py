@@ -137,7 +137,7 @@ def test_gemm_config3_shape_fused_vs_raw(R, B):
         assert bool((d <= 2.0 ** -7 * raw.float().abs() + 1e-6).all())
 
 
-@pytest.mark.parametrize("B", [2, 4, 8])
+@pytest.mark.parametrize("B", [1, 2, 4, 8])
 @pytest.mark.parametrize("table", ["matched", "laplace"])
 def test_gemm_config4_down_shape(R, B, table):
     """Config 4's W_down shape (5120 x 17408: 25 segments of 704 columns,
@@ -186,6 +186,30 @@ def test_gemm_config4_layer_pair_chained(R):
     _check(y1, ref1)
     ref2 = _reference(wd, ref1.to(torch.bfloat16), sd)
     _check(y2, ref2)
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_gemm_config4_four_layer_chain(R, B):
+    """Two config-4 layers in a row (W_up, W_down, W_up, W_down), the first
+    layer's matrices coded with their own tables and the second layer's
+    with a table from Laplace data (the bench's mismatched half), each
+    product fed the previous one's bf16 output.  Every stage is checked
+    against the float64 chain, whose intermediates are rounded to bf16 as
+    the kernel's outputs are."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: gemm four-layer chain B={B}")
+    lap_hist = D.exp_histogram(D.laplace_fp8_bytes(1 << 20, seed=59)[0])
+    shapes = [(17408, 5120), (5120, 17408), (17408, 5120), (5120, 17408)]
+    x = _x(B, 5120, seed=60 + B)
+    y, ref = x.cuda(), x.to(torch.float64)
+    for i, (rows, cols) in enumerate(shapes):
+        w, scale = _weights(rows, cols, seed=61 + i, dist="gaussian" if i % 2 == 0 else "laplace")
+        hist = D.exp_histogram(w) if i < 2 else lap_hist
+        m = T.encode_matrix(w, hist)
+        y = R.fp8_gemm_fused_tans(m.to("cuda"), m.decode_table().cuda(), y, scale)
+        assert y.shape == (B, rows)
+        ref = _reference(w, ref.to(torch.bfloat16), scale)
+        _check(y, ref)
 
 
 def test_gemm_argument_errors(R):

@@ -91,7 +91,8 @@ def test_table_device_matches_host(R, alphabet):
     check(lib.tans_build_decode_table_device(ctypes.c_void_p(sp.data_ptr()),
                                              ctypes.c_void_p(fr.data_ptr()), fr.numel(),
                                              spread.size.bit_length() - 1,
-                                             ctypes.c_void_p(dev.data_ptr()), None), "table")
+                                             ctypes.c_void_p(dev.data_ptr()), None, None),
+          "table")
     torch.cuda.synchronize()
     assert torch.equal(dev.cpu(), host)
 
@@ -112,10 +113,13 @@ def test_table_device_any_spread(R, alphabet):
     stream = torch.cuda.current_stream().cuda_stream
     sp_d = torch.from_numpy(sp).cuda()
     f_d = torch.from_numpy(f).cuda()
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
     assert lib.tans_build_decode_table_device(sp_d.data_ptr(), f_d.data_ptr(), nsym,
-                                              L.bit_length() - 1, dev.data_ptr(), stream) == 0
+                                              L.bit_length() - 1, dev.data_ptr(),
+                                              status.data_ptr(), stream) == 0
     torch.cuda.synchronize()
     assert torch.equal(dev.cpu(), host)
+    assert status.item() == 0
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
@@ -140,6 +144,100 @@ def test_decode_roundtrip(R, alphabet, K, N):
                             sp.cuda(), fr.cuda(), N)
     got = dec.cpu().t().contiguous()
     assert torch.equal(got, fp8), f"{(got != fp8).sum().item()} mismatched bytes"
+
+
+@pytest.mark.parametrize("alphabet,N", [("pair", 20), ("pair", 36), ("pair", 18),
+                                         ("pair", 52), ("nibble", 18), ("nibble", 34),
+                                         ("nibble", 66)])
+@pytest.mark.parametrize("K", [4096, 1000])
+def test_decode_last_tile_of_one_segment(R, alphabet, N, K):
+    """Streams whose last tile holds a single refill segment (pair: N % 16 =
+    2 or 4, nibble: N % 16 = 2, with N > 16), so the final refill check
+    follows the last segment of the tile before.  Uniformly random bytes
+    coded with the Qwen3 exponent table (which does not match them): many
+    lanes hold between the final check's threshold and 32 bits there, so a
+    decoder that gave them a word would shift the ranks of the lanes that
+    need one.  Decode returns the input."""
+    from rans_vectoradd import tans_codec as T
+    _say(f"case: gpu_tans_decode one-segment last tile K={K} N={N} {alphabet}")
+    g = torch.Generator().manual_seed(N * 7 + K)
+    fp8 = torch.randint(0, 256, (K, N), dtype=torch.uint8, generator=g)
+    exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
+    comp, st, off, part, sm, fr, sp = [x.cuda() for x in T.encode(fp8, exp_freqs,
+                                                                  alphabet=alphabet)]
+    dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
+    got = dec.cpu().t().contiguous()
+    assert torch.equal(got, fp8), f"{(got != fp8).sum().item()} mismatched bytes"
+
+
+def _invalid_tables(exp_probs, alphabet):
+    """(name, spread, freqs) triples the host builder rejects with
+    TANS_ETABLE."""
+    from rans_vectoradd import tans_codec as T
+    f = T.symbol_freqs(exp_probs, alphabet).astype(np.int32)
+    sp = T.build_spread(f).astype(np.int32)
+    out = []
+    if alphabet == "nibble":
+        # the rarest present symbol at frequency 1, the surplus on the most
+        # frequent one (the sum stays L)
+        g = f.copy()
+        i = int(np.argmax(g))
+        j = int(np.argmin(np.where(g > 0, g, 1 << 30)))
+        g[i] += g[j] - 1
+        g[j] = 1
+        out.append(("a present symbol at frequency 1", T.build_spread(g).astype(np.int32), g))
+    bad_sum = f.copy()
+    bad_sum[int(np.argmax(f))] += 1
+    out.append(("frequencies not summing to L", sp, bad_sum))
+    bad_sp = sp.copy()
+    bad_sp[5] = len(f) + 3
+    out.append(("a spread symbol outside the alphabet", bad_sp, f))
+    moved = sp.copy()
+    k = int(np.argmax(sp != sp[0]))
+    moved[k] = sp[0]              # one slot more for sp[0], one fewer for sp[k]
+    out.append(("slot counts differing from the frequencies", moved, f))
+    return out
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
+def test_table_device_rejects_what_the_host_rejects(R, alphabet):
+    """The device table build reports TANS_ETABLE through its status word
+    for each input the host builder rejects, and gpu_tans_decode raises
+    RuntimeError for it (the reference's TORCH_CHECKs in its table build,
+    csrc/tans_decode.cu:38,50); a valid pair keeps decoding after an
+    invalid one."""
+    from rans_vectoradd import tans_codec as T
+    from rans_vectoradd._lib import lib
+    L = 4096 if alphabet == "pair" else 2048
+    stream = torch.cuda.current_stream().cuda_stream
+    K, N = 256, 32
+    fp8 = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
+    exp_probs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
+    comp, st, off, part, sm, fr, sp = [x.cuda() for x in T.encode(fp8, exp_probs,
+                                                                  alphabet=alphabet)]
+    for name, bsp, bfr in _invalid_tables(R.QWEN3_14B_FP8_EXP, alphabet):
+        _say(f"case: invalid table ({alphabet}): {name}")
+        assert lib.tans_build_decode_table(bsp.ctypes.data, bfr.ctypes.data, len(bfr),
+                                           L.bit_length() - 1,
+                                           np.zeros(2 * L, np.uint32).ctypes.data) == -4
+        sp_d = torch.from_numpy(bsp).cuda()
+        f_d = torch.from_numpy(bfr).cuda()
+        tbl = torch.empty(2 * L, dtype=torch.int32, device="cuda")
+        status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        assert lib.tans_build_decode_table_device(sp_d.data_ptr(), f_d.data_ptr(), len(bfr),
+                                                  L.bit_length() - 1, tbl.data_ptr(),
+                                                  status.data_ptr(), stream) == 0
+        assert status.item() == -4, name
+        with pytest.raises(RuntimeError, match="valid decode table"):
+            R.gpu_tans_decode(comp, off, st, part, sm, sp_d, f_d, N)
+    dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
+    assert torch.equal(dec.cpu().t().contiguous(), fp8)
+    # an in-place change of a validated pair is checked again
+    fr_bad = fr.clone()
+    dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr_bad, N)
+    fr_bad[int(torch.argmax(fr_bad))] += 1
+    with pytest.raises(RuntimeError, match="valid decode table"):
+        R.gpu_tans_decode(comp, off, st, part, sm, sp, fr_bad, N)
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)

@@ -5,12 +5,16 @@ oracle/_ref/ (``make -C oracle ref``, run by ``__graft_entry__.build()`` where
 the reference is present).  Byte for byte on every output: compressed bytes,
 final states, block offsets and partial-slab counts.  Skipped where the
 compiled reference is absent."""
+import os
+
 import numpy as np
 import pytest
 
 from oracle import oracle as O
 
-pytestmark = pytest.mark.skipif(O.ref_lib() is None,
+# Only the path is checked at collection: the library is loaded by the tests
+# that run, so a process that deselects them (the GPU suite) never maps it.
+pytestmark = pytest.mark.skipif(not os.path.exists(O.REF_LIB_PATH),
                                 reason="oracle/_ref/libref_codec.so not built "
                                        "(needs the reference tree and torch's headers)")
 

@@ -9,9 +9,11 @@ start; the steps are cut into segments (step pairs with 2^12-state tables,
 nb <= 12; 3, 3 and 2 steps of every 8 with 2^11-state tables, nb <= 10);
 after every segment but the last a lane takes a word at <= 32 unread bits,
 after the second-to-last only below what the last segment can read (24 for
-pairs, 10 per step of the last segment otherwise).  The GPU encoder's
-output is checked byte for byte against the CPU encoder in
-tests/test_gpu_encode.py.
+pairs, 10 per step of the last segment otherwise) -- except when the last
+16-element tile (8 pair steps, 16 steps of the 3-3-2 schedule) holds a
+single segment: that check then follows the tile before and is the plain
+one.  The GPU encoder's output is checked byte for byte against the CPU
+encoder in tests/test_gpu_encode.py.
 """
 import random
 
@@ -31,8 +33,15 @@ def segments(S, triple):
     return out
 
 
+def tile_steps(triple):
+    return 16 if triple else 8
+
+
 def final_below(segs, triple):
     a, b = segs[-1]
+    ts = tile_steps(triple)
+    if b > ts and a == ts * ((b - 1) // ts):   # the last tile holds one segment
+        return 33
     return 10 * (b - a) if triple else 24
 
 
@@ -96,3 +105,54 @@ def test_segments_of_the_triple_schedule():
     assert segments(8, True) == [(0, 3), (3, 6), (6, 8)]
     assert segments(12, True) == [(0, 3), (3, 6), (6, 8), (8, 11), (11, 12)]
     assert segments(5, False) == [(0, 2), (2, 4), (4, 5)]
+
+
+# ---------------------------------------------------------------------------
+# Where the GPU decoders put the checks.  They decode 16-element tiles and
+# run every tile but the last through a path whose checks are all the plain
+# one; the last tile chooses per segment between the plain check, the final
+# check and none.  libtans_amd.so exports the thresholds both sides apply
+# (csrc/schedule.h: encoder_below, the rule csrc/codec.cpp encodes with, and
+# decoder_below, what that placement amounts to), compared here for every
+# stream length and with the rule as restated above.
+
+def _check_below():
+    import ctypes
+    from rans_vectoradd._lib import lib
+    fn = lib.tans_internal_check_below
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64]
+    return fn
+
+
+def restated_below(S, triple, j):
+    segs = segments(S, triple)
+    n = len(segs)
+    return 0 if j + 1 >= n else final_below(segs, triple) if j + 2 == n else 33
+
+
+def without_the_tile_rule(S, triple, j):
+    """The final threshold as the last segment's reach alone: with it the
+    check after segment n - 2 disagrees with the decoders' plain path
+    whenever the last tile holds a single segment."""
+    segs = segments(S, triple)
+    n = len(segs)
+    a, b = segs[-1]
+    return 0 if j + 1 >= n else (10 * (b - a) if triple else 24) if j + 2 == n else 33
+
+
+@pytest.mark.parametrize("triple", [False, True])
+def test_decoder_check_placement_matches_the_encoders(triple):
+    fn = _check_below()
+    ts = tile_steps(triple)
+    differs = set()
+    for S in range(1, 12 * ts + 1):
+        for j in range(len(segments(S, triple))):
+            enc, dec = fn(0, S, int(triple), j), fn(1, S, int(triple), j)
+            assert enc == dec == restated_below(S, triple, j), (S, j, enc, dec)
+            if without_the_tile_rule(S, triple, j) != dec:
+                differs.add(S % ts)
+    # exactly the streams whose last tile holds one segment: pair streams of
+    # 1 or 2 steps past whole tiles (N % 16 = 2 or 4, N > 16), 3-3-2 streams
+    # of 1-3 steps (N % 16 = 1..3)
+    assert differs == ({1, 2} if not triple else {1, 2, 3})
