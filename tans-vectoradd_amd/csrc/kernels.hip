@@ -1549,61 +1549,151 @@ __global__ __launch_bounds__(256) void gemm_raw_dot2_kernel(const v4u* __restric
         }
 }
 
-// Uncompressed FP8 skinny GEMM for B >= 2 (the baseline of the fused one
-// there), on the matrix cores as gemm_fused_kernel: a workgroup of nw
-// waves takes 16 rows,
-// and wave w the 64-column blocks w, w + nw, ... of them.  Lane j = 16 q + r
-// loads the 16 bytes of row r at column 64 k + 16 q (two k-blocks of 8, the
-// fused kernel's lane layout) and the matching 32 bytes of x[j % 16] from
-// global memory (cache-resident); the waves' 16 x 16 sums are added in wave
-// order through LDS, so results are deterministic.  C % 16 == 0.
+// Uncompressed FP8 skinny GEMM (the baseline of the fused one) on
+// v_mfma_f32_4x4x4_16b_bf16, whose 16 independent 4x4x4 blocks let one load
+// instruction cover 4 rows x 256 contiguous bytes.  Lane l = 4b + i holds
+// row i of a row group: of each 256-column chunk, columns 16b .. 16b + 15
+// (block b, four k-steps of 4 columns).  Lane 4b + j holds x[j] at the same
+// columns (and x[j + 4] for a second product when B > 4), loaded once per
+// chunk and used for all kRawGroups row groups of the wave; lanes j >= B
+// load zeros.  Block b's 4 x 4 sums cover its own columns and sit in lane
+// 4b + j, register i (row i, batch j).  A workgroup's waves take 4 *
+// kRawGroups rows and split the chunks in contiguous ranges; at the end the
+// 16 blocks are added by lane shuffles and the waves in wave order through
+// LDS, so results are deterministic.  C % 16 == 0; y's batch rows are ldy
+// apart (the launcher splits tall matrices into several launches).
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 constexpr int kRawMaxWaves = 16;
-constexpr int kRawUnroll = 4;   // column blocks whose loads a wave issues together
+constexpr int kRawGroups = 4;        // row groups of 4 rows per wave
+constexpr int kRawChunk = 256;       // columns per chunk
 
+// 4 bf16 from 4 FP8 bytes (exact).
+__device__ __forceinline__ v4bf fp8x4_to_bf16(uint32_t w) {
+    const v2bf p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    const v2bf p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+    return v4bf{p0[0], p0[1], p1[0], p1[1]};
+}
+
+template <bool HI>   // HI: B > 4, a second product for batch rows 4..7
+struct RawChunk {
+    v4u w[kRawGroups];   // 16 FP8 of each row group
+    v4u x[HI ? 4 : 2];   // 16 bf16 of x[j] (and x[j + 4])
+};
+
+template <bool HI>
 __global__ __launch_bounds__(kRawMaxWaves * kLanes) void gemm_raw_kernel(
-    const v4u* __restrict__ W, int64_t R, int64_t C, const v4u* __restrict__ x, int NB,
-    float scale, uint16_t* __restrict__ y) {
-    __shared__ v4f part[kRawMaxWaves][kLanes];
+    const uint8_t* __restrict__ W, int64_t R, int64_t C, const uint16_t* __restrict__ x, int NB,
+    float scale, uint16_t* __restrict__ y, int64_t ldy, int chunks_per_wave) {
+    constexpr int NP = HI ? 2 : 1;
+    __shared__ float part[kRawMaxWaves][kRawGroups][NP][16];
     const int lane = threadIdx.x & (kLanes - 1);
     const int wave = threadIdx.x / kLanes;
     const int nw = blockDim.x / kLanes;
-    const int q = lane >> 4, r = lane & 15;
-    const int bn = r < NB ? r : 0;                  // x row (lanes r >= NB: sums not stored)
-    const int64_t row0 = (int64_t)blockIdx.x * 16;
-    const int64_t row = row0 + r < R ? row0 + r : R - 1;
-    const int64_t cv = C / 16;                      // 16-byte vectors per W row
-    const v4u* wrow = W + row * cv;
-    const v4u* xrow = x + (int64_t)bn * (C / 8);    // 8 bf16 per 16-byte vector
-    const int64_t blocks = (C + 63) / 64;
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int64_t k0 = wave; k0 < blocks; k0 += (int64_t)nw * kRawUnroll) {
-        v4u wv[kRawUnroll], xa[kRawUnroll], xb[kRawUnroll];
-        #pragma unroll
-        for (int u = 0; u < kRawUnroll; u++) {
-            const int64_t k = k0 + (int64_t)u * nw;
-            const int64_t v = 4 * k + q;            // this lane's 16-byte vector of the row
-            const bool in = k < blocks && v < cv;   // wave-uniform k, per-lane column bound
-            wv[u] = in ? wrow[v] : v4u{0u, 0u, 0u, 0u};
-            xa[u] = in ? xrow[2 * v] : v4u{0u, 0u, 0u, 0u};
-            xb[u] = in ? xrow[2 * v + 1] : v4u{0u, 0u, 0u, 0u};
-        }
-        #pragma unroll
-        for (int u = 0; u < kRawUnroll; u++) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                fp8x8_to_bf16(wv[u].x, wv[u].y), __builtin_bit_cast(v8bf, xa[u]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                fp8x8_to_bf16(wv[u].z, wv[u].w), __builtin_bit_cast(v8bf, xb[u]), acc, 0, 0, 0);
-        }
-    }
-    part[wave][lane] = acc;
-    __syncthreads();
-    if (wave != 0 || r >= NB) return;
-    v4f t = part[0][lane];
-    for (int w = 1; w < nw; w++) t += part[w][lane];
+    const int b = lane >> 2, i = lane & 3;       // block; row (A) or batch row (x)
+    const int64_t row0 = (int64_t)blockIdx.x * (4 * kRawGroups);
+    const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
+    const int64_t c_begin = (int64_t)wave * chunks_per_wave;
+    const int64_t c_end = c_begin + chunks_per_wave < n_chunks ? c_begin + chunks_per_wave : n_chunks;
+    // Loads go through buffer resources (the launcher keeps R * C and B * C * 2
+    // below 2^31 bytes): a lane out of range reads at kNoSeg, past the bound,
+    // and gets zeros, so no load sits behind a branch and the wait counts stay
+    // exact across the two chunks in flight.
+    const Rsrc wsrc = rsrc(W, (uint32_t)(R * C));
+    const Rsrc xsrc = rsrc(x, (uint32_t)(NB * C * 2));
+    uint32_t woff[kRawGroups];
     #pragma unroll
-    for (int v = 0; v < 4; v++) {
-        const int64_t rr = row0 + 4 * q + v;        // lane j holds rows 4 (j / 16) + v
-        if (rr < R) y[(int64_t)r * R + rr] = bf16_rne(t[v] * scale);
+    for (int g = 0; g < kRawGroups; g++) {
+        const int64_t r = row0 + 4 * g + i;
+        woff[g] = (uint32_t)((r < R ? r : R - 1) * C + 16 * b);   // rows past R repeat the last one
+    }
+    const uint32_t xoff0 = (uint32_t)(((int64_t)i * C + 16 * b) * 2);
+    const uint32_t xoff1 = (uint32_t)(((int64_t)(i + 4) * C + 16 * b) * 2);
+    const bool x0_in = i < NB, x1_in = i + 4 < NB;
+    auto load = [&](int64_t c, RawChunk<HI>& k) {
+        const int64_t col = c * kRawChunk;
+        // C % 16 == 0: a lane's 16 columns are all in or all out
+        const bool in = c < c_end && col + 16 * b < C;
+        #pragma unroll
+        for (int g = 0; g < kRawGroups; g++)
+            k.w[g] = __builtin_amdgcn_raw_buffer_load_b128(
+                wsrc, in ? woff[g] + (uint32_t)col : kNoSeg, 0, kNT);
+        const uint32_t o0 = in && x0_in ? xoff0 + (uint32_t)col * 2u : kNoSeg;
+        k.x[0] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, o0, 0, 0);
+        k.x[1] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, o0, 16, 0);
+        if constexpr (HI) {
+            const uint32_t o1 = in && x1_in ? xoff1 + (uint32_t)col * 2u : kNoSeg;
+            k.x[2] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, o1, 0, 0);
+            k.x[3] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, o1, 16, 0);
+        }
+    };
+    v4f acc[kRawGroups][NP];
+    #pragma unroll
+    for (int g = 0; g < kRawGroups; g++)
+        #pragma unroll
+        for (int p = 0; p < NP; p++) acc[g][p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mma = [&](const RawChunk<HI>& k) {
+        #pragma unroll
+        for (int s = 0; s < 4; s++) {   // k-step: columns 16b + 4s .. + 3
+            const uint32_t xs[4] = {k.x[0].x, k.x[0].y, k.x[0].z, k.x[0].w};
+            const uint32_t xt[4] = {k.x[1].x, k.x[1].y, k.x[1].z, k.x[1].w};
+            const v2u x0 = s < 2 ? v2u{xs[2 * s], xs[2 * s + 1]} : v2u{xt[2 * s - 4], xt[2 * s - 3]};
+            v2u x1 = x0;
+            if constexpr (HI) {
+                const uint32_t xu[4] = {k.x[2].x, k.x[2].y, k.x[2].z, k.x[2].w};
+                const uint32_t xv[4] = {k.x[3].x, k.x[3].y, k.x[3].z, k.x[3].w};
+                x1 = s < 2 ? v2u{xu[2 * s], xu[2 * s + 1]} : v2u{xv[2 * s - 4], xv[2 * s - 3]};
+            }
+            #pragma unroll
+            for (int g = 0; g < kRawGroups; g++) {
+                const uint32_t ws[4] = {k.w[g].x, k.w[g].y, k.w[g].z, k.w[g].w};
+                const v4bf a = fp8x4_to_bf16(ws[s]);
+                acc[g][0] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
+                    a, __builtin_bit_cast(v4bf, x0), acc[g][0], 0, 0, 0);
+                if constexpr (HI)
+                    acc[g][NP - 1] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
+                        a, __builtin_bit_cast(v4bf, x1), acc[g][NP - 1], 0, 0, 0);
+            }
+        }
+    };
+    // two chunks in flight: one loads while the other multiplies (two
+    // buffers in turn, so no register copy waits on a pending load); chunks
+    // past c_end read zeros for W and x and add exact zeros
+    RawChunk<HI> k0, k1;
+    load(c_begin, k0);
+    for (int64_t c = c_begin; c < c_end; c += 2) {
+        load(c + 1, k1);
+        mma(k0);
+        load(c + 2, k0);
+        mma(k1);
+    }
+    // add the 16 blocks: lanes with equal lane mod 4 (every lane gets the sum)
+    #pragma unroll
+    for (int g = 0; g < kRawGroups; g++)
+        #pragma unroll
+        for (int p = 0; p < NP; p++)
+            #pragma unroll
+            for (int m = 4; m < kLanes; m <<= 1)
+                #pragma unroll
+                for (int v = 0; v < 4; v++) acc[g][p][v] += __shfl_xor(acc[g][p][v], m, kLanes);
+    if (lane < 4) {   // lane j: batch row j (and j + 4), register v: row v of the group
+        #pragma unroll
+        for (int g = 0; g < kRawGroups; g++)
+            #pragma unroll
+            for (int p = 0; p < NP; p++)
+                #pragma unroll
+                for (int v = 0; v < 4; v++) part[wave][g][p][4 * v + lane] = acc[g][p][v];
+    }
+    __syncthreads();
+    // 16 * kRawGroups * NP outputs (more than the threads of a one-wave
+    // workgroup when B > 4): each the waves' sums in wave order
+    for (int t = threadIdx.x; t < 16 * kRawGroups * NP; t += blockDim.x) {
+        const int g = t / (16 * NP), p = (t / 16) % NP, v = (t / 4) % 4, j = t % 4;
+        const int64_t row = row0 + 4 * g + v;
+        const int bn = j + 4 * p;
+        if (row >= R || bn >= NB) continue;
+        float sum = part[0][g][p][4 * v + j];
+        for (int w = 1; w < nw; w++) sum += part[w][g][p][4 * v + j];
+        y[(int64_t)bn * ldy + row] = bf16_rne(sum * scale);
     }
 }
 
@@ -1946,14 +2036,37 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
                            (const v4u*)w, R, C, (const v4u*)x, scale, (uint16_t*)y);
         return hip_check(hipGetLastError(), "gemm_raw_dot2_kernel launch");
     }
-    const int64_t blocks = (R + 15) / 16;
-    if (!grid_fits(blocks, kRawMaxWaves * kLanes)) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
-    // waves per workgroup: enough workgroups x waves to fill the GPU about
-    // twice (8192 waves), at most one wave per 64-column block
-    int nw = 1;
-    while (nw < kRawMaxWaves && blocks * nw < 8192 && nw * 64 < C) nw *= 2;
-    hipLaunchKernelGGL(gemm_raw_kernel, dim3((unsigned)blocks), dim3(nw * kLanes), 0, st,
-                       (const v4u*)w, R, C, (const v4u*)x, (int)B, scale, (uint16_t*)y);
+    // Workgroups of 4 * kRawGroups rows; their waves split the row's chunks
+    // in contiguous ranges.  Waves per workgroup: the most (up to 16) for
+    // which every workgroup is resident at once at 16 waves per CU, so no CU
+    // runs a second round of workgroups.
+    const int64_t rows_wg = 4 * kRawGroups;
+    const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
+    const int cus = cu_count();
+    if (cus <= 0) return fail(TANS_EHIP, "gemm_raw: cannot query the device's CU count");
+    if ((int64_t)B * C * 2 > INT32_MAX || C > INT32_MAX / rows_wg)
+        return fail(TANS_EINVAL, "gemm_raw: rows too long");
+    // launches of at most rows_per_launch rows keep each W slice below 2^31 bytes
+    const int64_t rows_per_launch = std::max<int64_t>(rows_wg, INT32_MAX / C / rows_wg * rows_wg);
+    for (int64_t r0 = 0; r0 < R; r0 += rows_per_launch) {
+        const int64_t rl = std::min(rows_per_launch, R - r0);
+        const int64_t blocks = (rl + rows_wg - 1) / rows_wg;
+        int64_t nw = kRawMaxWaves;
+        while (nw > 1 && (int64_t)cus * (kRawMaxWaves / nw) < blocks) nw--;
+        nw = std::min<int64_t>(nw, n_chunks);
+        const int64_t cpw = (n_chunks + nw - 1) / nw;        // chunks per wave
+        nw = (n_chunks + cpw - 1) / cpw;                      // waves with chunks
+        if (!grid_fits(blocks, kRawMaxWaves * kLanes))
+            return fail(TANS_EINVAL, "gemm_raw: matrix too large");
+        auto launch = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3((unsigned)(nw * kLanes)), 0,
+                               st, (const uint8_t*)w + r0 * C, rl, C, (const uint16_t*)x, (int)B,
+                               scale, (uint16_t*)y + r0, R, (int)cpw);
+        };
+        if (B > 4) launch(gemm_raw_kernel<true>); else launch(gemm_raw_kernel<false>);
+        const int rc = hip_check(hipGetLastError(), "gemm_raw_kernel launch");
+        if (rc != TANS_OK) return rc;
+    }
     return hip_check(hipGetLastError(), "gemm_raw_kernel launch");
 }
 

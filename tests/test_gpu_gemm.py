@@ -108,12 +108,33 @@ def test_gemm_fused_vector_input_and_determinism(R):
                                          (17, 80, 5), (40, 1040, 4), (7, 1040, 1)])
 def test_gemm_raw_vs_float64(R, rows, cols, B):
     """Both raw kernels (row-streaming at B = 1, matrix cores from B = 2),
-    including rows not a multiple of 16 and widths not a multiple of 64."""
+    including rows not a multiple of 16 (the last workgroup's rows past R)
+    and widths not a multiple of 256 (a partial last chunk)."""
     _say(f"case: fp8_gemm_raw {rows}x{cols} B={B}")
     w, scale = _weights(rows, cols, seed=7)
     x = _x(B, cols, seed=8)
     y = R.fp8_gemm_raw(w.cuda(), x.cuda(), scale)
     _check(y, _reference(w, x, scale))
+
+
+@pytest.mark.parametrize("B", [3, 8])
+def test_gemm_raw_several_launches(R, B):
+    """A W above 2^31 bytes (131077 x 16400): the raw kernel's launcher
+    splits the rows into launches that each address less than 2^31 bytes
+    (130944 rows, then 133).  Rows at the start, around the split and at
+    the end are checked against float64."""
+    rows, cols = 131077, 16400
+    _say(f"case: fp8_gemm_raw {rows}x{cols} B={B} (two launches)")
+    g = torch.Generator(device="cuda").manual_seed(B)
+    w = torch.randint(0, 256, (rows, cols), dtype=torch.uint8, device="cuda", generator=g)
+    w = torch.where((w & 0x7F) == 0x7F, torch.zeros_like(w), w)     # no NaN bytes
+    x = _x(B, cols, seed=B + 5).cuda()
+    y = R.fp8_gemm_raw(w, x, 0.5)
+    for lo, hi in ((0, 64), (130900, 131000), (rows - 64, rows)):
+        ref = _reference(w[lo:hi].cpu(), x.cpu(), 0.5)
+        _check(y[:, lo:hi], ref)
+    del w
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("B", [1, 8])
