@@ -57,7 +57,9 @@ HBM_PEAK_GBS = 8000.0
 N_ELEMS = 1 << 29
 HEADLINE_LANE = 1024                 # 64Ki-element streams
 DECODE_ELEMS = 1 << 30               # config 2
-SWEEP_LANES = (16, 64, 256, 1024)    # 1Ki, 4Ki, 16Ki, 64Ki streams
+# 1Ki, 4Ki, 8Ki, 16Ki, 64Ki streams of 64 lanes; 128 per lane is the length of the
+# reference's shortest stream (128 FP8 bytes per thread, bench_vecadd.py:105-111)
+SWEEP_LANES = (16, 64, 128, 256, 1024)
 SETTLE_S = 0.3                       # seconds of back-to-back calls before timing
 POWER_S = 3.0                        # seconds of power/clock sampling per headline kernel
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fused_vecadd_64ki_pair_traffic.txt")
