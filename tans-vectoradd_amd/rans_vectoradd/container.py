@@ -13,13 +13,16 @@ the metadata key ``tans:name`` with a JSON description:
   for a TansMatrix (the layout of fp8_gemm_fused_tans).
 
 Plain tensors (scales, unencoded weights) are stored under their own names;
-``tans_format`` in the metadata names the layout version: v3 streams follow
+``tans_format`` in the metadata names the layout version: v4 streams follow
 the carry-driven refill schedule (segments of two steps for the pair
 alphabet; 3, 3 and 2 steps for the nibble alphabet, whose tables give every
-present symbol a frequency of at least 2) and matrices the 16-row
-matrix-core lane groups (include/tans_amd.h).  v2 files are read when all
-their entries use the pair alphabet (its layout is unchanged); files of
-other versions, and v2 files with nibble entries, are refused.
+present symbol a frequency of at least 2) with a plain check before a last
+16-element tile of one segment, and matrices the 16-row matrix-core lane
+groups (include/tans_amd.h).  v3 files are read unless an entry of lanes has
+such a last tile (N > 16 and N % 16 in 1..4 with pairs, 1..3 with nibbles:
+there v3 applied the final check), v2 files under the same condition when
+all their entries use the pair alphabet; files of other versions are
+refused.
 """
 from __future__ import annotations
 
@@ -29,8 +32,19 @@ import torch
 
 from .tans_codec import TansMatrix, TansTensor
 
-FORMAT = "tans-wave64-v3"
-_PAIR_ONLY = "tans-wave64-v2"   # the pair layout is unchanged since this version
+FORMAT = "tans-wave64-v4"
+_PREV = "tans-wave64-v3"        # differs only where _last_tile_rule_changed
+_PAIR_ONLY = "tans-wave64-v2"   # pair entries: as v3
+
+
+def _last_tile_rule_changed(desc: dict) -> bool:
+    """An entry whose streams end in a 16-element tile of one refill segment
+    (where v4 made the check before it the plain one).  Matrices never do:
+    each lane holds a multiple of 8 elements."""
+    if desc.get("kind") != "lanes":
+        return False
+    N = int(desc["N"])
+    return N > 16 and 1 <= N % 16 <= (4 if desc.get("alphabet") == "pair" else 3)
 _PARTS = ("comp", "states", "offsets", "sm", "freqs", "spread")
 
 
@@ -78,7 +92,7 @@ def load(path: str, device="cpu") -> dict:
     with safe_open(path, framework="pt", device="cpu") as f:
         meta = f.metadata() or {}
         fmt = meta.get("tans_format")
-        if fmt not in (FORMAT, _PAIR_ONLY):
+        if fmt not in (FORMAT, _PREV, _PAIR_ONLY):
             raise ValueError(f"{path}: not a {FORMAT} container (format {fmt!r}); "
                              "re-encode it with this version")
         keys = set(f.keys())
@@ -87,6 +101,11 @@ def load(path: str, device="cpu") -> dict:
             raise ValueError(f"{path}: {fmt} container with nibble-alphabet entries, whose "
                              "streams follow the previous refill schedule; re-encode it with "
                              "this version")
+        changed = [n for n, d in encoded.items() if _last_tile_rule_changed(d)]
+        if fmt != FORMAT and changed:
+            raise ValueError(f"{path}: {fmt} container whose entries {changed} end in a tile of "
+                             "one refill segment, where that version's last check differs; "
+                             "re-encode them with this version")
         for name, desc in encoded.items():
             parts = {p: f.get_tensor(f"{name}.{p}").to(device) for p in _PARTS}
             keys -= {f"{name}.{p}" for p in _PARTS}

@@ -85,7 +85,8 @@ def test_container_rejects_other_files(tmp_path):
 
 def test_container_reads_v2_pair_entries_only(tmp_path):
     """v2 containers differ from v3 only in the nibble alphabet's refill
-    schedule: their pair entries load, a nibble entry is refused."""
+    schedule: their pair entries load (at lengths the v4 change leaves
+    alone), a nibble entry is refused."""
     from safetensors import safe_open
     from safetensors.torch import save_file
     from rans_vectoradd import container, data as D, tans_codec as T
@@ -105,6 +106,36 @@ def test_container_reads_v2_pair_entries_only(tmp_path):
         else:
             with pytest.raises(ValueError, match="re-encode"):
                 container.load(v2)
+
+
+def test_container_reads_v3_unless_the_last_tile_rule_changed(tmp_path):
+    """v3 containers differ from v4 only for entries of lanes whose last
+    16-element tile holds one refill segment (N > 16 and N % 16 in 1..4 with
+    pairs, 1..3 with nibbles): such entries are refused, the others load; a v2
+    pair entry at such a length is refused too."""
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+    from rans_vectoradd import container, data as D, tans_codec as T
+    cases = [("pair", 32, True), ("pair", 20, False), ("pair", 18, False), ("pair", 22, True),
+             ("pair", 4, True), ("nibble", 34, False), ("nibble", 36, True)]
+    for alphabet, N, ok in cases:
+        q, _ = D.gaussian_fp8_bytes(64 * N, seed=N)
+        t = T.TansTensor.from_tuple(T.encode(q.reshape(64, N), D.exp_histogram(q),
+                                             alphabet=alphabet), 64, N, alphabet)
+        path = os.path.join(tmp_path, f"{alphabet}{N}.safetensors")
+        container.save(path, {"w": t})
+        with safe_open(path, framework="pt") as f:
+            meta, tensors = f.metadata(), {k: f.get_tensor(k) for k in f.keys()}
+        assert meta["tans_format"] == "tans-wave64-v4"
+        for old in ("tans-wave64-v3", "tans-wave64-v2") if alphabet == "pair" else ("tans-wave64-v3",):
+            meta["tans_format"] = old
+            prev = os.path.join(tmp_path, f"{alphabet}{N}_{old[-2:]}.safetensors")
+            save_file(tensors, prev, metadata=meta)
+            if ok:
+                assert torch.equal(container.load(prev)["w"].comp, t.comp)
+            else:
+                with pytest.raises(ValueError, match="one refill segment"):
+                    container.load(prev)
 
 
 def _checkpoint(path):
