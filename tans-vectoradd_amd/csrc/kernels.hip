@@ -43,7 +43,8 @@
 // word and whose bound is the buffer's end, once the segment's ring slot is
 // free.  The loaded segment stays in registers and is written into the
 // ring at the next stage whose slot is free, which comes no later than the
-// stage in which a lane could first take one of its words.  A stage is at
+// stage in which a lane could first take one of its words.  Slots past a
+// stream's end are never written: no lane takes a word there.  A stage is at
 // most four refill checks, so at most 256 words are handed out per stage, and
 // kSlots = kDelay + 2 slots guarantee that a fetched segment starts more
 // than a stage's worth of words ahead of the lanes.  Lanes out of range
@@ -336,6 +337,7 @@ struct Feed {
     uint32_t len_b;         // bytes in the stream (clamped to the buffer)
     uint32_t next_slot;     // ring slot of the next segment
     uint32_t dest;          // ring slot of the pending segment
+    uint32_t pend_new;      // 1 while the pending segment is not in the ring
     uint32_t handed;        // words handed to lanes so far
     uint32_t ring_b;        // byte offset in the ring of word `handed`
     uint32_t ring_w;        // LDS word index of the ring, held in a VGPR (see refill)
@@ -402,31 +404,34 @@ __device__ __forceinline__ void feed_fetch(Feed& f, const uint32_t* comp, int64_
     }
 }
 
-// The last of the first segments becomes the pending one (see feed_stage).
+// Slots past the stream's end stay unwritten (wave-uniform tests).  The last
+// of the first segments becomes the pending one, already in the ring (see
+// feed_stage).
 __device__ __forceinline__ void feed_commit(Feed& f, int lane, const Seg (&first)[kSlots],
                                             Seg& pend) {
     #pragma unroll
-    for (int i = 0; i < kSlots; i++) write_seg(f.ring, i, first[i], lane);
+    for (int i = 0; i < kSlots; i++)
+        if (i == 0 || (uint32_t)(i * kSegWords * 4) < f.len_b) write_seg(f.ring, i, first[i], lane);
     pend = first[kSlots - 1];
     f.dest = kSlots - 1;
+    f.pend_new = 0u;
 }
 
 // Start of a stage.  The next segment's slot is free once every word of the
 // segment kSlots earlier in the stream has been handed out.  Then the
-// pending segment (the last one fetched) is written to its slot, and the
-// next segment, when the stream has it, is fetched into the pending
-// registers.  Slots are written only here and from the pending registers,
-// so when nothing was fetched since the pending segment was written, its
-// slot already holds it and writing it again changes nothing.  A fetched
-// segment waits in registers until the next stage whose slot is free: its
-// load has a stage or more to arrive, and the lanes, which take at most
-// kChecksPerStage * 64 words per stage, reach its first word no earlier
-// than the stage after that one.
+// pending segment (the last one fetched), unless it is in the ring already,
+// is written to its slot, and the next segment, when the stream has it, is
+// fetched into the pending registers.  A fetched segment waits in registers
+// until the next stage whose slot is free: its load has a stage or more to
+// arrive, and the lanes, which take at most kChecksPerStage * 64 words per
+// stage, reach its first word no earlier than the stage after that one.
 __device__ __forceinline__ void feed_stage(Feed& f, Seg& pend, int lane) {
     static_assert(kDelay == 1, "one pending segment per stream");
     if (f.next_b <= 4u * f.handed + (uint32_t)((kSlots - 1) * kSegWords * 4)) {   // wave-uniform
-        write_seg(f.ring, f.dest, pend, lane);
+        if (f.pend_new) write_seg(f.ring, f.dest, pend, lane);
+        f.pend_new = 0u;
         if (f.next_b < f.len_b) {
+            f.pend_new = 1u;
             pend = fetch_seg(f, f.next_b, lane);
             f.dest = f.next_slot;
             f.next_b += (uint32_t)(kSegWords * 4);
