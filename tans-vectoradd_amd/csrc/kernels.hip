@@ -9,7 +9,7 @@
 //                            add's launch shape (bandwidth ceilings)
 //   table_kernel             decode table from device spread/freqs
 //                            (csrc/tans_decode.cu:23-59 without the host trip)
-//   fused_add_kernel<SPS,G>  decode two encodings + FP8 add
+//   fused_add_kernel<SPS,G,OT> decode two encodings + FP8 add
 //                            (csrc/vecadd.cu:156-243)
 //   decode_kernel<SPS>       decode to FP8 bytes [N, K]
 //                            (csrc/tans_decode.cu:125-155)
@@ -382,6 +382,7 @@ __device__ __forceinline__ void write_seg(uint32_t* ring, uint32_t slot, Seg v, 
 // stream offsets of all their chains before the first call, so those scalar
 // loads share one round trip too.  lds0 is the start of the workgroup's LDS
 // (the decode table).
+template <int NSEG = kSlots>
 __device__ __forceinline__ void feed_fetch(Feed& f, const uint32_t* comp, int64_t words,
                                            int64_t s, int64_t e, uint32_t* ring,
                                            const void* lds0, int lane, Seg (&first)[kSlots]) {
@@ -398,7 +399,7 @@ __device__ __forceinline__ void feed_fetch(Feed& f, const uint32_t* comp, int64_
     f.ring_w = in_vgpr((uint32_t)(reinterpret_cast<const char*>(ring) -
                                   reinterpret_cast<const char*>(lds0)) / 4u);
     #pragma unroll
-    for (int i = 0; i < kSlots; i++) {
+    for (int i = 0; i < NSEG; i++) {
         const uint32_t b = (uint32_t)(i * kSegWords * 4);
         first[i] = fetch_seg(f, b < f.len_b ? b : kNoSeg, lane);
     }
@@ -406,13 +407,15 @@ __device__ __forceinline__ void feed_fetch(Feed& f, const uint32_t* comp, int64_
 
 // Slots past the stream's end stay unwritten (wave-uniform tests).  The last
 // of the first segments becomes the pending one, already in the ring (see
-// feed_stage).
+// feed_stage).  With NSEG < kSlots (streams known to fit NSEG segments,
+// decoded without feed_stage) only those are loaded and written.
+template <int NSEG = kSlots>
 __device__ __forceinline__ void feed_commit(Feed& f, int lane, const Seg (&first)[kSlots],
                                             Seg& pend) {
     #pragma unroll
-    for (int i = 0; i < kSlots; i++)
+    for (int i = 0; i < NSEG; i++)
         if (i == 0 || (uint32_t)(i * kSegWords * 4) < f.len_b) write_seg(f.ring, i, first[i], lane);
-    pend = first[kSlots - 1];
+    if constexpr (NSEG == kSlots) pend = first[kSlots - 1];
     f.dest = kSlots - 1;
     f.pend_new = 0u;
 }
@@ -642,6 +645,10 @@ struct Alpha {
     // the final check's fin_pos when the stream ends with a whole tile
     static constexpr uint32_t kFinPosFullTile =
         32u - (uint32_t)(kTriple ? tans_sched::kTripleMaxNb * 2 : tans_sched::kPairFinalBelow);
+    // ring segments that hold a whole one-tile stream: under the refill
+    // schedule a lane takes at most 3 words over 8 pair steps (768 bytes per
+    // group) and at most 5 over 16 nibble steps (1280 bytes)
+    static constexpr int kOneTileSegs = kTriple ? 2 : 1;
 };
 
 // Segments of S steps in the last tile and the final check's fin_pos
@@ -713,8 +720,9 @@ struct Chains {
 // final segments, last_segs of them (the rest of the tile decodes past the
 // end: no checks there, so it reads only the lane's own window and the
 // table, and its bytes are discarded); fin_pos sets the final check
-// (check_last).
-template <int SPS, int C, bool LAST>
+// (check_last).  RESIDENT: the streams were loaded whole at their start
+// (feed_commit<NSEG>), so no stage fetches.
+template <int SPS, int C, bool LAST, bool RESIDENT = false>
 __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ tbl, int lane,
                                          uint32_t (&ex)[C][4],
                                          int last_segs = Alpha<SPS>::kSegsPerTile,
@@ -724,8 +732,10 @@ __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ 
     for (int c = 0; c < C; c++) ch.l[c].q &= 0xF800001Fu;
     static_for<0, A::kStagesPerTile>([&](auto H) {
         constexpr int h = decltype(H)::value;
-        #pragma unroll
-        for (int c = 0; c < C; c++) feed_stage(ch.f[c], ch.p[c], lane);
+        if constexpr (!RESIDENT) {
+            #pragma unroll
+            for (int c = 0; c < C; c++) feed_stage(ch.f[c], ch.p[c], lane);
+        }
         uint32_t e[C][8];
         static_for<0, A::kSegsPerStage>([&](auto Q) {
             constexpr int q = decltype(Q)::value;
@@ -774,7 +784,9 @@ __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ 
 // loaded once per CU, and short streams (down to one tile per lane) do not
 // pay a workgroup launch and a table load per group.
 // ---------------------------------------------------------------------
-template <int SPS, int G>
+// OT: every stream is one tile, loaded whole at its start (no stage
+// fetches, no sign/mantissa prefetch).
+template <int SPS, int G, bool OT>
 struct FusedWave {
     static constexpr int C = 2 * G;   // chain 2g: A of group g, 2g + 1: B of group g
     Chains<C> ch;
@@ -795,7 +807,7 @@ struct FusedWave {
     template <int P, bool LAST>
     __device__ __forceinline__ void tile(int t) {
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex);
+        dec_tile<SPS, C, LAST, OT>(ch, tbl, lane, ex);
         pace(progress, lane, (uint32_t)(base + t), live);
         #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -814,6 +826,7 @@ struct FusedWave {
         // sign/mantissa of tile t + kSmAhead.  The loads are unconditional (the
         // wait counts stay exact); past the last tile they have an empty bound
         // and read nothing.
+        if constexpr (OT) return;
         const bool sm_next = t + kSmAhead < n_tiles;   // wave-uniform
         #pragma unroll
         for (int c = 0; c < C; c++)
@@ -826,7 +839,7 @@ struct FusedWave {
     }
 };
 
-template <int SPS, int G>
+template <int SPS, int G, bool OT>
 __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     const uint32_t* __restrict__ a_comp, int64_t a_words, const int64_t* __restrict__ a_off,
     const uint16_t* __restrict__ a_st, const v2u* __restrict__ a_sm,
@@ -849,7 +862,9 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
     const bool live = g0 < n_groups;   // wave-uniform
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * G;
-    FusedWave<SPS, G> w;
+    constexpr int NSEG = OT ? Alpha<SPS>::kOneTileSegs : kSlots;   // segments loaded at a start
+    constexpr int NSM = OT ? 1 : kSmAhead;                           // sm tiles loaded at a start
+    FusedWave<SPS, G, OT> w;
     w.progress = &smem.progress;
     w.live = (uint32_t)(wg_groups >= (int64_t)kDecWaves * G ? kDecWaves : (wg_groups + G - 1) / G);
     w.lane = lane;
@@ -873,10 +888,10 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             w.sm_bytes[j] = (uint32_t)lanes * 8u;
             w.out_cur[j] = reinterpret_cast<char*>(out + k0);
             const int64_t sa = a_off[g], ea = a_off[g + 1], sb = b_off[g], eb = b_off[g + 1];
-            feed_fetch(w.ch.f[2 * j], a_comp, a_words, sa, ea, smem.rings[wave][2 * j], tbl,
-                       lane, first[2 * j]);
-            feed_fetch(w.ch.f[2 * j + 1], b_comp, b_words, sb, eb, smem.rings[wave][2 * j + 1],
-                       tbl, lane, first[2 * j + 1]);
+            feed_fetch<NSEG>(w.ch.f[2 * j], a_comp, a_words, sa, ea, smem.rings[wave][2 * j],
+                             tbl, lane, first[2 * j]);
+            feed_fetch<NSEG>(w.ch.f[2 * j + 1], b_comp, b_words, sb, eb,
+                             smem.rings[wave][2 * j + 1], tbl, lane, first[2 * j + 1]);
             st0[2 * j] = a_st[k0 + lane_ld];
             st0[2 * j + 1] = b_st[k0 + lane_ld];
             glanes[j] = lanes;
@@ -886,7 +901,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             for (int s = 0; s < 2; s++) {
                 const int c = 2 * j + s;
                 #pragma unroll
-                for (int i = 0; i < kSmAhead; i++) {
+                for (int i = 0; i < NSM; i++) {
                     const int64_t ti = i < n_tiles ? i : n_tiles - 1;
                     w.sm[c][i] = __builtin_amdgcn_raw_buffer_load_b64(
                         rsrc(rows[s] + ti * w.sm_stride, i < n_tiles ? w.sm_bytes[j] : 0u),
@@ -906,7 +921,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     for (;;) {
         #pragma unroll
         for (int c = 0; c < C; c++) {
-            feed_commit(w.ch.f[c], lane, first[c], w.ch.p[c]);
+            feed_commit<NSEG>(w.ch.f[c], lane, first[c], w.ch.p[c]);
             lane_init(w.ch.l[c], w.ch.f[c], lane, glanes[c / 2], st0[c], L, smem.sink_off());
         }
         w.base = done;
@@ -1893,14 +1908,18 @@ int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes, const int64_
     if (cus <= 0) return fail(TANS_EHIP, "vecadd_fused: cannot query the device's CU count");
     const int64_t blocks = std::min<int64_t>((groups + per_block - 1) / per_block, cus);
     const int n_tiles = (int)(N / kTile);
-#define TANS_LAUNCH_FUSED(S)                                                                      \
-    hipLaunchKernelGGL((fused_add_kernel<S, kFusedGroups<S>>), dim3((unsigned)blocks),              \
+#define TANS_LAUNCH_FUSED(S, OT)                                                                  \
+    hipLaunchKernelGGL((fused_add_kernel<S, kFusedGroups<S>, OT>), dim3((unsigned)blocks),          \
                        dim3(kDecBlock), 0, (hipStream_t)stream, (const uint32_t*)a_comp,         \
                        a_comp_bytes / 4, a_offsets, a_states, (const v2u*)a_sm,                  \
                        (const uint32_t*)b_comp, b_comp_bytes / 4, b_offsets, b_states,           \
                        (const v2u*)b_sm, (const v2u*)table, K, n_tiles, (v4u*)out)
-    if (sps == 2) TANS_LAUNCH_FUSED(2);
-    else TANS_LAUNCH_FUSED(1);
+    // streams of one tile are loaded whole at their start (fused_add_kernel<.., true>)
+    if (sps == 2) {
+        if (n_tiles == 1) TANS_LAUNCH_FUSED(2, true); else TANS_LAUNCH_FUSED(2, false);
+    } else {
+        if (n_tiles == 1) TANS_LAUNCH_FUSED(1, true); else TANS_LAUNCH_FUSED(1, false);
+    }
 #undef TANS_LAUNCH_FUSED
     return hip_check(hipGetLastError(), "fused_add_kernel launch");
 }

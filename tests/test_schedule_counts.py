@@ -83,6 +83,44 @@ def closed_form(nbs, triple):
     return t + (1 if 32 * t - c2 < final_below(segs, triple) else 0)
 
 
+def max_words(S, triple, top_nb):
+    """The most words one lane can take over S steps of at most top_nb bits
+    each, over every way the bits can fall (the rule of replay(), by
+    dynamic programming over the bits the lane holds)."""
+    segs = segments(S, triple)
+    states = {64: 2}   # bits held -> most words taken so far
+    for q, (a, b) in enumerate(segs):
+        nxt = {}
+        for held, taken in states.items():
+            for c in range(0, min(held, (b - a) * top_nb) + 1):
+                h, t = held - c, taken
+                if q + 1 < len(segs):
+                    below = final_below(segs, triple) if q + 2 == len(segs) else 33
+                    if h < below:
+                        h, t = h + 32, t + 1
+                nxt[h] = max(nxt.get(h, 0), t)
+        states = nxt
+    return max(states.values())
+
+
+@pytest.mark.parametrize("triple,top_nb,ring_segments", [(False, 12, 1), (True, 10, 2)])
+def test_one_tile_streams_fit_the_first_segments(triple, top_nb, ring_segments):
+    """fused_add_kernel<..., OT = true> loads a stream of one 16-element tile
+    whole at its start into Alpha::kOneTileSegs ring segments of 256 words
+    (1 for pairs, 2 for nibbles) and never fetches again: 64 lanes of at
+    most 3 (pair) or 5 (nibble) words fit.  The DP agrees with replay() on
+    the sequences that reach the bound."""
+    worst = 0
+    for S in range(1, tile_steps(triple) + 1):
+        w = max_words(S, triple, top_nb)
+        assert 64 * w <= 256 * ring_segments, (S, w)
+        worst = max(worst, w)
+    assert worst == (5 if triple else 3)
+    S = tile_steps(triple)
+    assert max(replay([top_nb] * S, triple), replay([0] * S, triple)) <= worst
+    assert max_words(S, triple, top_nb) >= replay([top_nb] * S, triple)
+
+
 @pytest.mark.parametrize("triple,top_nb", [(False, 12), (True, 10)])
 def test_closed_form_equals_replay(triple, top_nb):
     rng = random.Random(7)
