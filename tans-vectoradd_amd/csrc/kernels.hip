@@ -9,7 +9,7 @@
 //                            add's launch shape (bandwidth ceilings)
 //   table_kernel             decode table from device spread/freqs
 //                            (csrc/tans_decode.cu:23-59 without the host trip)
-//   fused_add_kernel<SPS,G,OT> decode two encodings + FP8 add
+//   fused_add_kernel<SPS,G,FIRST> decode two encodings + FP8 add
 //                            (csrc/vecadd.cu:156-243)
 //   decode_kernel<SPS>       decode to FP8 bytes [N, K]
 //                            (csrc/tans_decode.cu:125-155)
@@ -649,6 +649,10 @@ struct Alpha {
     // schedule a lane takes at most 3 words over 8 pair steps (768 bytes per
     // group) and at most 5 over 16 nibble steps (1280 bytes)
     static constexpr int kOneTileSegs = kTriple ? 2 : 1;
+    // the most tiles whose streams fit the ring's kSlots segments: a lane
+    // takes at most 12 words over 32 pair steps (3072 bytes per group) and
+    // at most 10 over 32 nibble steps (2560 bytes)
+    static constexpr int kResidentTiles = kTriple ? 2 : 4;
 };
 
 // Segments of S steps in the last tile and the final check's fin_pos
@@ -784,10 +788,12 @@ __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ 
 // loaded once per CU, and short streams (down to one tile per lane) do not
 // pay a workgroup launch and a table load per group.
 // ---------------------------------------------------------------------
-// OT: every stream is one tile, loaded whole at its start (no stage
-// fetches, no sign/mantissa prefetch).
-template <int SPS, int G, bool OT>
+// FIRST > 0: every stream fits FIRST ring segments and is loaded whole at
+// its start, with its (at most kSmAhead) sign/mantissa tiles: no stage
+// fetches, no sign/mantissa prefetch.  FIRST = 0: streams of any length.
+template <int SPS, int G, int FIRST>
 struct FusedWave {
+    static constexpr bool RES = FIRST > 0;
     static constexpr int C = 2 * G;   // chain 2g: A of group g, 2g + 1: B of group g
     Chains<C> ch;
     v2u sm[C][kSmAhead];    // sign/mantissa words of tiles t .. t + kSmAhead - 1 (by t mod kSmAhead)
@@ -807,7 +813,7 @@ struct FusedWave {
     template <int P, bool LAST>
     __device__ __forceinline__ void tile(int t) {
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST, OT>(ch, tbl, lane, ex);
+        dec_tile<SPS, C, LAST, RES>(ch, tbl, lane, ex);
         pace(progress, lane, (uint32_t)(base + t), live);
         #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -826,7 +832,7 @@ struct FusedWave {
         // sign/mantissa of tile t + kSmAhead.  The loads are unconditional (the
         // wait counts stay exact); past the last tile they have an empty bound
         // and read nothing.
-        if constexpr (OT) return;
+        if constexpr (RES) return;
         const bool sm_next = t + kSmAhead < n_tiles;   // wave-uniform
         #pragma unroll
         for (int c = 0; c < C; c++)
@@ -839,7 +845,7 @@ struct FusedWave {
     }
 };
 
-template <int SPS, int G, bool OT>
+template <int SPS, int G, int FIRST>
 __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     const uint32_t* __restrict__ a_comp, int64_t a_words, const int64_t* __restrict__ a_off,
     const uint16_t* __restrict__ a_st, const v2u* __restrict__ a_sm,
@@ -862,9 +868,13 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
     const bool live = g0 < n_groups;   // wave-uniform
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * G;
-    constexpr int NSEG = OT ? Alpha<SPS>::kOneTileSegs : kSlots;   // segments loaded at a start
-    constexpr int NSM = OT ? 1 : kSmAhead;                           // sm tiles loaded at a start
-    FusedWave<SPS, G, OT> w;
+    constexpr int NSEG = FIRST > 0 ? FIRST : kSlots;   // segments loaded at a start
+    constexpr int NSM = FIRST == Alpha<SPS>::kOneTileSegs ? 1 : kSmAhead;   // sm tiles loaded then
+    static_assert(FIRST == 0 || FIRST == Alpha<SPS>::kOneTileSegs || FIRST == kSlots,
+                  "one-tile streams, streams of up to kResidentTiles tiles, or any");
+    static_assert(Alpha<SPS>::kResidentTiles <= kSmAhead,
+                  "a resident stream's sign/mantissa tiles are all loaded at its start");
+    FusedWave<SPS, G, FIRST> w;
     w.progress = &smem.progress;
     w.live = (uint32_t)(wg_groups >= (int64_t)kDecWaves * G ? kDecWaves : (wg_groups + G - 1) / G);
     w.lane = lane;
@@ -1908,17 +1918,21 @@ int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes, const int64_
     if (cus <= 0) return fail(TANS_EHIP, "vecadd_fused: cannot query the device's CU count");
     const int64_t blocks = std::min<int64_t>((groups + per_block - 1) / per_block, cus);
     const int n_tiles = (int)(N / kTile);
-#define TANS_LAUNCH_FUSED(S, OT)                                                                  \
-    hipLaunchKernelGGL((fused_add_kernel<S, kFusedGroups<S>, OT>), dim3((unsigned)blocks),          \
+#define TANS_LAUNCH_FUSED(S, FIRST)                                                               \
+    hipLaunchKernelGGL((fused_add_kernel<S, kFusedGroups<S>, FIRST>), dim3((unsigned)blocks),       \
                        dim3(kDecBlock), 0, (hipStream_t)stream, (const uint32_t*)a_comp,         \
                        a_comp_bytes / 4, a_offsets, a_states, (const v2u*)a_sm,                  \
                        (const uint32_t*)b_comp, b_comp_bytes / 4, b_offsets, b_states,           \
                        (const v2u*)b_sm, (const v2u*)table, K, n_tiles, (v4u*)out)
-    // streams of one tile are loaded whole at their start (fused_add_kernel<.., true>)
+    // streams that fit the ring are loaded whole at their start
     if (sps == 2) {
-        if (n_tiles == 1) TANS_LAUNCH_FUSED(2, true); else TANS_LAUNCH_FUSED(2, false);
+        if (n_tiles == 1) TANS_LAUNCH_FUSED(2, Alpha<2>::kOneTileSegs);
+        else if (n_tiles <= Alpha<2>::kResidentTiles) TANS_LAUNCH_FUSED(2, kSlots);
+        else TANS_LAUNCH_FUSED(2, 0);
     } else {
-        if (n_tiles == 1) TANS_LAUNCH_FUSED(1, true); else TANS_LAUNCH_FUSED(1, false);
+        if (n_tiles == 1) TANS_LAUNCH_FUSED(1, Alpha<1>::kOneTileSegs);
+        else if (n_tiles <= Alpha<1>::kResidentTiles) TANS_LAUNCH_FUSED(1, kSlots);
+        else TANS_LAUNCH_FUSED(1, 0);
     }
 #undef TANS_LAUNCH_FUSED
     return hip_check(hipGetLastError(), "fused_add_kernel launch");

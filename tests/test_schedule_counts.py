@@ -105,8 +105,8 @@ def max_words(S, triple, top_nb):
 
 @pytest.mark.parametrize("triple,top_nb,ring_segments", [(False, 12, 1), (True, 10, 2)])
 def test_one_tile_streams_fit_the_first_segments(triple, top_nb, ring_segments):
-    """fused_add_kernel<..., OT = true> loads a stream of one 16-element tile
-    whole at its start into Alpha::kOneTileSegs ring segments of 256 words
+    """fused_add_kernel<..., FIRST = kOneTileSegs> loads a stream of one
+    16-element tile whole at its start into that many ring segments of 256 words
     (1 for pairs, 2 for nibbles) and never fetches again: 64 lanes of at
     most 3 (pair) or 5 (nibble) words fit.  The DP agrees with replay() on
     the sequences that reach the bound."""
@@ -119,6 +119,18 @@ def test_one_tile_streams_fit_the_first_segments(triple, top_nb, ring_segments):
     S = tile_steps(triple)
     assert max(replay([top_nb] * S, triple), replay([0] * S, triple)) <= worst
     assert max_words(S, triple, top_nb) >= replay([top_nb] * S, triple)
+
+
+@pytest.mark.parametrize("triple,top_nb,tiles", [(False, 12, 4), (True, 10, 2)])
+def test_resident_streams_fit_the_ring(triple, top_nb, tiles):
+    """fused_add_kernel<..., FIRST = kSlots> loads streams of up to
+    Alpha::kResidentTiles tiles (4 for pairs, 2 for nibbles) whole into the
+    ring's 3 segments of 256 words: 64 lanes of at most 12 words fit, and
+    one more tile would not."""
+    for S in range(1, tiles * tile_steps(triple) + 1):
+        assert 64 * max_words(S, triple, top_nb) <= 3 * 256, S
+    S = (tiles + 1) * tile_steps(triple)
+    assert 64 * max_words(S, triple, top_nb) > 3 * 256
 
 
 @pytest.mark.parametrize("triple,top_nb", [(False, 12), (True, 10)])
