@@ -11,7 +11,7 @@
 //                            (csrc/tans_decode.cu:23-59 without the host trip)
 //   fused_add_kernel<SPS,G,FIRST> decode two encodings + FP8 add
 //                            (csrc/vecadd.cu:156-243)
-//   decode_kernel<SPS>       decode to FP8 bytes [N, K]
+//   decode_kernel<SPS,FIRST> decode to FP8 bytes [N, K]
 //                            (csrc/tans_decode.cu:125-155)
 //   gemm_fused_kernel<SPS>   decode W + skinny GEMM partial sums on the
 //                            matrix cores (no counterpart in the
@@ -1010,9 +1010,11 @@ struct DecodeSmem {
 static_assert(sizeof(DecodeSmem<2>) <= 160 * 1024 && sizeof(DecodeSmem<1>) <= 160 * 1024,
               "decoder LDS exceeds the 160 KiB of a gfx950 CU");
 
-template <int SPS>
+// FIRST as in FusedWave: > 0 for streams loaded whole at their start.
+template <int SPS, int FIRST>
 struct DecodeWave {
     static constexpr int C = kDecodeGroups;
+    static constexpr bool RES = FIRST > 0;
     Chains<C> ch;
     v2u sm[C][kSmAhead];    // sign/mantissa words of tiles t .. t + kSmAhead - 1 (by t mod kSmAhead)
     const char* pf[C];      // sign/mantissa row of the next prefetch (wave-uniform)
@@ -1043,7 +1045,7 @@ struct DecodeWave {
         // symbol come after every real one (no refill checks there), stay
         // inside the table, and their bytes are not stored.
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST>(ch, tbl, lane, ex, last_segs, fin_pos);
+        dec_tile<SPS, C, LAST, RES>(ch, tbl, lane, ex, last_segs, fin_pos);
         pace(progress, lane, (uint32_t)(base + t), live);
         uint32_t w[C][4];
         #pragma unroll
@@ -1103,6 +1105,7 @@ struct DecodeWave {
             }
         }
         out_tile += kTile * K;
+        if constexpr (RES) return;   // every sign/mantissa tile was loaded at the start
         // sign/mantissa of tile min(t + kSmAhead, n_tiles - 1): the loads are
         // unconditional and, unlike FusedWave::tile, keep their bound past the
         // last tile (a select there costs this kernel two SGPRs, which it
@@ -1139,7 +1142,7 @@ struct DecodeWave {
 };
 
 
-template <int SPS>
+template <int SPS, int FIRST>
 __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     const uint32_t* __restrict__ comp, int64_t words, const int64_t* __restrict__ off,
     const uint16_t* __restrict__ st, const v2u* __restrict__ sm,
@@ -1159,7 +1162,11 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * C;
     const bool live = g0 < n_groups;   // wave-uniform
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * C;
-    DecodeWave<SPS> w;
+    constexpr int NSEG = FIRST > 0 ? FIRST : kSlots;   // as in fused_add_kernel
+    constexpr int NSM = FIRST == Alpha<SPS>::kOneTileSegs ? 1 : kSmAhead;
+    static_assert(FIRST == 0 || FIRST == Alpha<SPS>::kOneTileSegs || FIRST == kSlots,
+                  "one-tile streams, streams of up to kResidentTiles tiles, or any");
+    DecodeWave<SPS, FIRST> w;
     w.progress = &smem.progress;
     w.live = (uint32_t)(wg_groups >= (int64_t)kDecWaves * C ? kDecWaves : (wg_groups + C - 1) / C);
     w.lane = lane;
@@ -1197,12 +1204,12 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
             const bool active = lane < lanes;
             const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
             w.sm_bytes[j] = (uint32_t)lanes * 8u;
-            feed_fetch(w.ch.f[j], comp, words, os[j], oe[j], smem.rings[wave][j], tbl, lane,
-                       first[j]);
+            feed_fetch<NSEG>(w.ch.f[j], comp, words, os[j], oe[j], smem.rings[wave][j], tbl,
+                             lane, first[j]);
             st0[j] = st[k0 + lane_ld];
             const char* row = reinterpret_cast<const char*>(sm + k0);
             #pragma unroll
-            for (int i = 0; i < kSmAhead; i++) {
+            for (int i = 0; i < NSM; i++) {
                 const int64_t ti = i < w.n_tiles ? i : w.n_tiles - 1;
                 w.sm[j][i] = __builtin_amdgcn_raw_buffer_load_b64(
                     rsrc(row + ti * w.sm_stride, i < w.n_tiles ? w.sm_bytes[j] : 0u),
@@ -1222,7 +1229,7 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     for (;;) {
         #pragma unroll
         for (int j = 0; j < C; j++) {
-            feed_commit(w.ch.f[j], lane, first[j], w.ch.p[j]);
+            feed_commit<NSEG>(w.ch.f[j], lane, first[j], w.ch.p[j]);
             lane_init(w.ch.l[j], w.ch.f[j], lane, w.lanes[j], st0[j], L, smem.sink_off());
         }
         w.base = done;
@@ -1968,13 +1975,21 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
         blocks = std::min<int64_t>(blocks, cus);
     }
     if (!grid_fits(blocks, kDecBlock)) return fail(TANS_EINVAL, "decode: K too large");
-#define TANS_LAUNCH_DECODE(S)                                                                     \
-    hipLaunchKernelGGL((decode_kernel<S>), dim3((unsigned)blocks),                               \
+#define TANS_LAUNCH_DECODE(S, FIRST)                                                              \
+    hipLaunchKernelGGL((decode_kernel<S, FIRST>), dim3((unsigned)blocks),                        \
                        dim3(kDecBlock), 0, (hipStream_t)stream, (const uint32_t*)comp,           \
                        comp_bytes / 4, offsets, states, (const v2u*)sm, (const v2u*)table, K, N, \
                        (uint8_t*)out)
-    if (sps == 2) TANS_LAUNCH_DECODE(2);
-    else TANS_LAUNCH_DECODE(1);
+    // streams that fit the ring are loaded whole at their start
+    const int64_t n_tiles = (N + kTile - 1) / kTile;
+    if (sps == 2) {
+        if (n_tiles == 1) TANS_LAUNCH_DECODE(2, Alpha<2>::kOneTileSegs);
+        else if (n_tiles <= Alpha<2>::kResidentTiles) TANS_LAUNCH_DECODE(2, kSlots);
+        else TANS_LAUNCH_DECODE(2, 0);
+    } else {   // (the nibble decoder loaded whole at two tiles spills registers)
+        if (n_tiles == 1) TANS_LAUNCH_DECODE(1, Alpha<1>::kOneTileSegs);
+        else TANS_LAUNCH_DECODE(1, 0);
+    }
 #undef TANS_LAUNCH_DECODE
     return hip_check(hipGetLastError(), "decode_kernel launch");
 }

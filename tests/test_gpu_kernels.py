@@ -242,7 +242,7 @@ def test_table_device_rejects_what_the_host_rejects(R, alphabet):
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
 @pytest.mark.parametrize("K,N", [(1024, 128), (10000, 256), (1024, 1024), (64, 16), (70, 32),
-                                 (4160, 64), (130, 80)])
+                                 (4160, 64), (130, 80), (1, 16), (5, 64), (127, 32)])
 def test_vecadd_fused_vs_raw_and_oracle(R, lut, alphabet, K, N):
     """Streams of 1 tile (N = 16: one or two ring segments loaded at a
     group's start), of up to 4 tiles with pairs and 2 with nibbles (the whole
