@@ -886,7 +886,24 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     uint16_t st0[C];
     int glanes[G];
     // the loads of the groups gbase .. gbase + G - 1
-    auto setup = [&](int64_t gbase) {
+    // With resident streams a wave switches groups every few tiles, and the
+    // switch waits on the next group's stream offsets: they are loaded
+    // during the last tile instead, by lanes 0-3 (a vector load, so the
+    // tile's own waits do not include it), and read with v_readlane.
+    // (not in the nibble kernel for two-tile streams: it has no VGPRs to spare)
+    constexpr bool AHEAD = FIRST > 0 && (SPS == 2 || FIRST == Alpha<SPS>::kOneTileSegs);
+    static_assert(G == 1 || !AHEAD, "offsets ahead for one group per wave");
+    int64_t noff = 0;
+    auto next_offsets = [&](int64_t gnext) {
+        const int64_t g = gnext < n_groups ? gnext : n_groups - 1;
+        if (lane < 4) noff = (lane < 2 ? a_off : b_off)[g + (lane & 1)];
+    };
+    auto noff_lane = [&](int l) {
+        const uint32_t lo = (uint32_t)noff, hi = (uint32_t)((uint64_t)noff >> 32);
+        return (int64_t)(((uint64_t)__builtin_amdgcn_readlane(hi, l) << 32) |
+                         __builtin_amdgcn_readlane(lo, l));
+    };
+    auto setup = [&](int64_t gbase, bool ahead) {
         #pragma unroll
         for (int j = 0; j < G; j++) {
             // a wave past the last group repeats it with no lanes in range
@@ -897,7 +914,12 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
             w.sm_bytes[j] = (uint32_t)lanes * 8u;
             w.out_cur[j] = reinterpret_cast<char*>(out + k0);
-            const int64_t sa = a_off[g], ea = a_off[g + 1], sb = b_off[g], eb = b_off[g + 1];
+            int64_t sa, ea, sb, eb;
+            if (ahead) {
+                sa = noff_lane(0); ea = noff_lane(1); sb = noff_lane(2); eb = noff_lane(3);
+            } else {
+                sa = a_off[g]; ea = a_off[g + 1]; sb = b_off[g]; eb = b_off[g + 1];
+            }
             feed_fetch<NSEG>(w.ch.f[2 * j], a_comp, a_words, sa, ea, smem.rings[wave][2 * j],
                              tbl, lane, first[2 * j]);
             feed_fetch<NSEG>(w.ch.f[2 * j + 1], b_comp, b_words, sb, eb,
@@ -922,7 +944,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             }
         }
     };
-    setup(g0);
+    setup(g0, false);
     table_store<L>(tbl, tr);
     if (threadIdx.x == 0) smem.init();
     __syncthreads();
@@ -945,6 +967,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             if (t + 3 < body) w.template tile<3, false>(t + 3);
         }
         static_assert(kSmAhead == 4, "the loop above is unrolled for kSmAhead == 4");
+        if constexpr (AHEAD) next_offsets(g0 + grid_groups);
         switch (body % kSmAhead) {
             case 0: w.template tile<0, true>(body); break;
             case 1: w.template tile<1, true>(body); break;
@@ -954,7 +977,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
         done += n_tiles;
         g0 += grid_groups;
         if (g0 >= n_groups) break;
-        setup(g0);
+        setup(g0, AHEAD);
     }
 }
 
