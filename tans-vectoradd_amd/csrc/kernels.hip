@@ -375,8 +375,10 @@ __device__ __forceinline__ void write_seg(uint32_t* ring, uint32_t slot, Seg v, 
 }
 
 // Clamp a group's stream (words s .. e of comp) to the buffer and fetch its
-// first kSlots segments into `first` (nothing for those past the stream's
-// end); feed_commit writes them to the ring.  The two halves let a kernel
+// first NSEG segments (kSlots, or fewer for streams known to fit them) into
+// `first`: segments past the stream's end are loads with an empty range,
+// which read nothing.  feed_commit writes them to the ring.  The two halves
+// let a kernel
 // issue these loads together with the decode table's, so the stream and the
 // table cost one memory round trip before decoding starts.  Callers read the
 // stream offsets of all their chains before the first call, so those scalar
