@@ -453,6 +453,37 @@ def test_streams_consumed_near_the_feed_limit(R, lut, alphabet):
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("N", [16, 32, 48, 64, 80])
+def test_longest_short_streams(R, lut, alphabet, N):
+    """Streams at the most words a lane can take: every exponent 15, coded
+    with a table for p_e proportional to 2^-e, so each step reads the most
+    bits the table allows (12 with pairs, 10 with nibbles).  Up to 4 tiles
+    (pairs) or 2 (nibbles) the kernels load such streams whole at a group's
+    start; past that they fetch by stage.  Decode returns the input and the
+    fused add equals the raw add and the oracle's table."""
+    from rans_vectoradd import tans_codec as T
+    _say(f"case: longest streams N={N} {alphabet}")
+    K = 461   # 7 full groups and one of 13 lanes
+    g = torch.Generator().manual_seed(N)
+    sm = torch.randint(0, 16, (2, K, N), dtype=torch.uint8, generator=g)
+    sm = torch.where((sm & 7) == 7, sm - 1, sm)          # mantissa 7 with exponent 15 is NaN
+    fa, fb = ((sm & 8) << 4) | (15 << 3) | (sm & 7)
+    steep = torch.tensor([2.0 ** -e for e in range(16)], dtype=torch.float64)
+    ea = T.encode(fa, steep, tile=8, alphabet=alphabet)
+    eb = T.encode(fb, steep, tile=8, alphabet=alphabet)
+    comp, st, off, part, smp, fr, sp = [x.cuda() for x in ea]
+    dec = R.gpu_tans_decode(comp, off, st, part, smp, sp, fr, N)
+    assert torch.equal(dec.cpu().t().contiguous(), fa)
+    tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy())
+    order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
+    args = [x.cuda() for x in (*[ea[i] for i in order], *[eb[i] for i in order], tbl)]
+    fused = T.untile(R.fp8_vecadd_fused_tans(*args, N).cpu(), K, N)
+    raw = R.fp8_vecadd_raw(fa.flatten().cuda(), fb.flatten().cuda()).cpu().reshape(K, N)
+    assert torch.equal(fused, raw)
+    assert np.array_equal(fused.numpy(), O.vecadd(lut, fa.numpy(), fb.numpy()).reshape(K, N))
+
+
+@pytest.mark.parametrize("alphabet", ALPHABETS)
 def test_decoders_replay_in_a_hip_graph(R, alphabet):
     """The fused add and the standalone decode (with its device table build)
     captured in one HIP graph: every replay, with eager launches and host
