@@ -1563,20 +1563,28 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-template <int NB>
+// KS waves of a workgroup (of 4) take the same rows, each a contiguous
+// range of column blocks, and add their sums in wave order through LDS: a
+// matrix of few, long rows (5120 x 17408) then still runs enough waves.
+template <int NB, int KS>
 __global__ __launch_bounds__(256) void gemm_raw_dot2_kernel(const v4u* __restrict__ W, int64_t R,
                                                        int64_t C, const v4u* __restrict__ x,
                                                        float scale, uint16_t* __restrict__ y) {
+    static_assert(KS == 1 || KS == 2 || KS == 4, "a workgroup is 4 waves");
+    __shared__ float part[256 / kLanes][kRawRows][NB];
     const int lane = threadIdx.x & (kLanes - 1);
-    const int64_t r0 = ((int64_t)blockIdx.x * (256 / kLanes) + threadIdx.x / kLanes) * kRawRows;
-    if (r0 >= R) return;
+    const int wave = threadIdx.x / kLanes;
+    const int ks = wave % KS;
+    const int64_t r0 = ((int64_t)blockIdx.x * (256 / kLanes / KS) + wave / KS) * kRawRows;
     const int64_t cb = C / 16;                 // 16-column blocks per row
+    const int64_t kb = (cb + KS - 1) / KS;     // of them per wave
+    const int64_t k_end = std::min<int64_t>((int64_t)(ks + 1) * kb, cb);
     float acc[kRawRows][NB];
     #pragma unroll
     for (int i = 0; i < kRawRows; i++)
         #pragma unroll
         for (int b = 0; b < NB; b++) acc[i][b] = 0.0f;
-    for (int64_t k = lane; k < cb; k += kLanes) {
+    for (int64_t k = (int64_t)ks * kb + lane; k < k_end && r0 < R; k += kLanes) {
         v2bf wb[kRawRows][8];
         #pragma unroll
         for (int i = 0; i < kRawRows; i++) {
@@ -1607,8 +1615,24 @@ __global__ __launch_bounds__(256) void gemm_raw_dot2_kernel(const v4u* __restric
         #pragma unroll
         for (int b = 0; b < NB; b++) {
             const float v = wave_sum(acc[i][b]);
-            if (lane == 0 && r0 + i < R) y[b * R + r0 + i] = bf16_rne(v * scale);
+            if (KS == 1) {
+                if (lane == 0 && r0 + i < R) y[b * R + r0 + i] = bf16_rne(v * scale);
+            } else if (lane == 0) {
+                part[wave][i][b] = v;
+            }
         }
+    if constexpr (KS > 1) {
+        __syncthreads();
+        if (ks == 0 && lane < kRawRows * NB) {
+            const int i = lane / NB, b = lane % NB;
+            if (r0 + i < R) {
+                float t = part[wave][i][b];
+                #pragma unroll
+                for (int q = 1; q < KS; q++) t += part[wave + q][i][b];
+                y[b * R + r0 + i] = bf16_rne(t * scale);
+            }
+        }
+    }
 }
 
 // Uncompressed FP8 skinny GEMM (the baseline of the fused one) on
@@ -2107,11 +2131,20 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
         return fail(TANS_EINVAL, "gemm_raw: W and x must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
     if (B == 1) {
-        const int64_t rows_per_block = (256 / kLanes) * kRawRows;
+        // split each row over 2 or 4 waves, about 2.5 KiB or more of it each
+        // (17408 x 5120: 2 waves, 16.4 against 17.2 us per call on MI355X;
+        // 5120 x 17408: 4 waves, 17.4 against 24.1 us)
+        const int ks = C >= 10240 ? 4 : C >= 5120 ? 2 : 1;
+        const int64_t rows_per_block = (256 / kLanes) / ks * kRawRows;
         const int64_t blocks = (R + rows_per_block - 1) / rows_per_block;
         if (!grid_fits(blocks, 256)) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
-        hipLaunchKernelGGL((gemm_raw_dot2_kernel<1>), dim3((unsigned)blocks), dim3(256), 0, st,
-                           (const v4u*)w, R, C, (const v4u*)x, scale, (uint16_t*)y);
+        auto launch = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(256), 0, st, (const v4u*)w, R,
+                               C, (const v4u*)x, scale, (uint16_t*)y);
+        };
+        if (ks == 1) launch(gemm_raw_dot2_kernel<1, 1>);
+        else if (ks == 2) launch(gemm_raw_dot2_kernel<1, 2>);
+        else launch(gemm_raw_dot2_kernel<1, 4>);
         return hip_check(hipGetLastError(), "gemm_raw_dot2_kernel launch");
     }
     // Workgroups of 4 * kRawGroups rows; their waves split the row's chunks

@@ -105,11 +105,14 @@ def test_gemm_fused_vector_input_and_determinism(R):
 
 @pytest.mark.parametrize("rows,cols,B", [(2176, 1280, 1), (2176, 1280, 8), (100, 64, 3),
                                          (5120, 17408 // 4, 2), (5, 16, 2), (33, 48, 8),
-                                         (17, 80, 5), (40, 1040, 4), (7, 1040, 1)])
+                                         (17, 80, 5), (40, 1040, 4), (7, 1040, 1),
+                                         (37, 5136, 1), (9, 10256, 1), (70, 12000, 1)])
 def test_gemm_raw_vs_float64(R, rows, cols, B):
     """Both raw kernels (row-streaming at B = 1, matrix cores from B = 2),
     including rows not a multiple of 16 (the last workgroup's rows past R)
-    and widths not a multiple of 256 (a partial last chunk)."""
+    and widths not a multiple of 256 (a partial last chunk).  At B = 1 rows
+    of 5120 columns or more are split over 2 waves, of 10240 or more over 4
+    (uneven splits at 5136, 10256 and 12000 columns)."""
     _say(f"case: fp8_gemm_raw {rows}x{cols} B={B}")
     w, scale = _weights(rows, cols, seed=7)
     x = _x(B, cols, seed=8)
