@@ -1649,8 +1649,8 @@ __global__ __launch_bounds__(256) void gemm_raw_dot2_kernel(const v4u* __restric
 // LDS, so results are deterministic.  C % 16 == 0; y's batch rows are ldy
 // apart (the launcher splits tall matrices into several launches).
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-constexpr int kRawMaxWaves = 16;
-constexpr int kRawGroups = 4;        // row groups of 4 rows per wave
+constexpr int kRawMaxWaves = 8;      // waves per workgroup (up to 256 VGPRs each)
+constexpr int kRawGroups = 5;        // row groups of 4 rows per wave: 20 rows a workgroup
 constexpr int kRawChunk = 256;       // columns per chunk
 
 // 4 bf16 from 4 FP8 bytes (exact).
@@ -2148,9 +2148,13 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
         return hip_check(hipGetLastError(), "gemm_raw_dot2_kernel launch");
     }
     // Workgroups of 4 * kRawGroups rows; their waves split the row's chunks
-    // in contiguous ranges.  Waves per workgroup: the most (up to 16) for
-    // which every workgroup is resident at once at 16 waves per CU, so no CU
-    // runs a second round of workgroups.
+    // in contiguous ranges.  Up to one workgroup per CU (5120 rows: 256
+    // workgroups of 20 rows on MI355X) takes 8 waves each; more workgroups
+    // take 3, so that 4 or 5 of them share a CU and every one is resident
+    // at once (17408 rows: 871 workgroups).  Measured on 5120 x 17408 at
+    // B = 2 / 4 / 8: 17.8 / 19.2 / 24.0 us, against 24.8 / 27.8 / 36.2 us with
+    // 16-row workgroups (320 of them, so 64 CUs held two); on 17408 x 5120:
+    // 19.1 / 20.7 / 25.8 against 19.7 / 21.9 / 28.1 us.
     const int64_t rows_wg = 4 * kRawGroups;
     const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
     const int cus = cu_count();
@@ -2162,8 +2166,7 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
     for (int64_t r0 = 0; r0 < R; r0 += rows_per_launch) {
         const int64_t rl = std::min(rows_per_launch, R - r0);
         const int64_t blocks = (rl + rows_wg - 1) / rows_wg;
-        int64_t nw = kRawMaxWaves;
-        while (nw > 1 && (int64_t)cus * (kRawMaxWaves / nw) < blocks) nw--;
+        int64_t nw = blocks <= cus ? kRawMaxWaves : 3;
         nw = std::min<int64_t>(nw, n_chunks);
         const int64_t cpw = (n_chunks + nw - 1) / nw;        // chunks per wave
         nw = (n_chunks + cpw - 1) / cpw;                      // waves with chunks
