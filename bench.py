@@ -60,6 +60,7 @@ DECODE_ELEMS = 1 << 30               # config 2
 # 1Ki, 4Ki, 8Ki, 16Ki, 64Ki streams of 64 lanes; 128 per lane is the length of the
 # reference's shortest stream (128 FP8 bytes per thread, bench_vecadd.py:105-111)
 SWEEP_LANES = (16, 64, 128, 256, 1024)
+PACKED_MAX_LANE = 64                 # lanes up to this length take the packed layout (pair)
 SETTLE_S = 0.3                       # seconds of back-to-back calls before timing
 POWER_S = 3.0                        # seconds of power/clock sampling per headline kernel
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fused_vecadd_64ki_pair_traffic.txt")
@@ -92,6 +93,10 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--policy", choices=("nt", "default"), default="nt",
                    help="load/store policy of --profile read/write/stream21")
     p.add_argument("--batch", type=int, default=1, help="batch of --profile gemm/gemm_raw")
+    p.add_argument("--lane", type=int, default=HEADLINE_LANE,
+                   help="elements per lane of --profile fused (16 * 2^k, up to 1024)")
+    p.add_argument("--layout", choices=("auto", "words", "packed"), default="auto",
+                   help="stream layout of --profile fused (packed: pair, lanes <= 64)")
     p.add_argument("--power", type=float, default=0.0,
                    help="with --profile: launch back to back for this many seconds while "
                         "sampling board power and GFX clock (amd-smi)")
@@ -162,18 +167,25 @@ def make_inputs(seed: int):
     return out[0], out[1], hist
 
 
-def encode_pair(qa_d, qb_d, hist, lane: int, alphabet: str):
-    """Encode a and b with the GPU encoder (the same bytes as the CPU one);
-    returns the device argument list of fp8_vecadd_fused_tans, the
-    compressed byte count and the encode time of both."""
+def encode_pair(qa_d, qb_d, hist, lane: int, alphabet: str, layout: str = "auto"):
+    """Encode a and b with the GPU encoder (the same bytes as the CPU one),
+    or, where encode() picks the packed layout of short streams (pair
+    alphabet, at most 64 elements per lane), with the CPU encoder; returns
+    the device argument list of fp8_vecadd_fused_tans, the compressed byte
+    count and the encode time of both."""
     import torch
     from rans_vectoradd import tans_codec as T
 
     K = N_ELEMS // lane
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ea = T.encode_gpu(qa_d.reshape(K, lane), hist, tile=8, alphabet=alphabet)
-    eb = T.encode_gpu(qb_d.reshape(K, lane), hist, tile=8, alphabet=alphabet)
+    if T.packed_layout(lane, alphabet, layout):
+        h = hist.cpu().numpy()
+        ea = [x.cuda() for x in T.encode(qa_d.cpu().reshape(K, lane), h, alphabet=alphabet)]
+        eb = [x.cuda() for x in T.encode(qb_d.cpu().reshape(K, lane), h, alphabet=alphabet)]
+    else:
+        ea = T.encode_gpu(qa_d.reshape(K, lane), hist, tile=8, alphabet=alphabet)
+        eb = T.encode_gpu(qb_d.reshape(K, lane), hist, tile=8, alphabet=alphabet)
     torch.cuda.synchronize()
     t_enc = time.perf_counter() - t0
     tbl = T.build_decode_table(ea[6].cpu().numpy(), ea[5].cpu().numpy()).cuda()
@@ -206,7 +218,7 @@ def gpu_encode_rate(q_d, hist, lane: int, alphabet: str, reps: int = 5) -> dict:
 
 def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps: int,
                      warmup: int, settle_s: float, raw_fn=None, rounds: int = 1,
-                     power_s: float = 0.0) -> dict:
+                     power_s: float = 0.0, layout: str = "auto") -> dict:
     """One fused configuration.  With raw_fn, the raw kernel and the fused
     one are timed in alternation for `rounds` rounds of `steps` launches each
     (raw first), so both see the same clocks and board temperature; the
@@ -216,8 +228,10 @@ def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps:
     import torch
     import rans_vectoradd as R
 
+    from rans_vectoradd import tans_codec as T
+
     K = N_ELEMS // lane
-    args, in_bytes, t_enc = encode_pair(qa_d, qb_d, hist, lane, alphabet)
+    args, in_bytes, t_enc = encode_pair(qa_d, qb_d, hist, lane, alphabet, layout)
     hbm_bytes = in_bytes + N_ELEMS                       # + the output write
     fn = lambda: R.fp8_vecadd_fused_tans(*args, lane)    # noqa: E731
     out = fn()
@@ -246,6 +260,7 @@ def run_fused_config(qa_d, qb_d, raw_out, hist, lane: int, alphabet: str, steps:
     del args
     torch.cuda.empty_cache()
     return extra | {"stream_elems": 64 * lane, "lane_elems": lane, "alphabet": alphabet,
+            "layout": "packed" if T.packed_layout(lane, alphabet, layout) else "words",
             "kernel_ms": kernel_ms, "step_ms": step_ms, "api_host_us": host_us,
             "bits_per_byte": in_bytes * 8 / (2 * N_ELEMS), "hbm_bytes": hbm_bytes,
             "encode_s": t_enc, "exact_vs_raw": exact,
@@ -645,8 +660,8 @@ def profile_only(args) -> None:
         elif args.profile == "stream21":
             fn = lambda: C.stream_probe("stream21", qa, qb, out=buf, nontemporal=nt)   # noqa: E731
         else:
-            dev_args, _, _ = encode_pair(qa, qb, hist, HEADLINE_LANE, args.alphabet)
-            fn = lambda: R.fp8_vecadd_fused_tans(*dev_args, HEADLINE_LANE)   # noqa: E731
+            dev_args, _, _ = encode_pair(qa, qb, hist, args.lane, args.alphabet, args.layout)
+            fn = lambda: R.fp8_vecadd_fused_tans(*dev_args, args.lane)   # noqa: E731
     n = settle(fn, args.settle)
     if args.power:
         print(json.dumps({"profile": args.profile, "power": power_sample(fn, args.power)}))
@@ -736,18 +751,20 @@ def main() -> None:
     raw_out = R.fp8_vecadd_raw(qa, qb)
     raw_fn = lambda: R.fp8_vecadd_raw(qa, qb)   # noqa: E731
 
-    configs = [(HEADLINE_LANE, "pair")]
+    configs = [(HEADLINE_LANE, "pair", "auto")]
     if not args.no_sweep:
-        configs += [(ln, "pair") for ln in SWEEP_LANES if ln != HEADLINE_LANE]
-        configs += [(HEADLINE_LANE, "nibble")]
+        configs += [(ln, "pair", "auto") for ln in SWEEP_LANES if ln != HEADLINE_LANE]
+        configs += [(HEADLINE_LANE, "nibble", "auto")]
+        # the short streams again in the refill-schedule layout, for comparison
+        configs += [(ln, "pair", "words") for ln in SWEEP_LANES if ln <= PACKED_MAX_LANE]
     results = []
     raw_kernel = raw_step = None
-    for i, (lane, alph) in enumerate(configs):
-        log(f"fused: stream {64 * lane} elements ({lane} per lane), {alph}"
+    for i, (lane, alph, layout) in enumerate(configs):
+        log(f"fused: stream {64 * lane} elements ({lane} per lane), {alph}, layout {layout}"
             + ("; raw and fused timed in alternation, 3 rounds" if i == 0 else ""))
         r = run_fused_config(qa, qb, raw_out, hist, lane, alph, args.steps, args.warmup,
                              args.settle, raw_fn=raw_fn if i == 0 else None, rounds=3,
-                             power_s=0.0 if args.no_power else POWER_S)
+                             power_s=0.0 if args.no_power else POWER_S, layout=layout)
         if i == 0:
             raw_kernel, raw_step = r["raw_kernel_ms"], r["raw_step_ms"]
             for k, v in (r.get("power") or {}).items():
@@ -808,7 +825,7 @@ def main() -> None:
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": read_traffic()},
-        "sweep": [{k: r[k] for k in ("stream_elems", "lane_elems", "alphabet", "kernel_ms",
+        "sweep": [{k: r[k] for k in ("stream_elems", "lane_elems", "alphabet", "layout", "kernel_ms",
                                      "step_ms", "bits_per_byte", "eff_gbs", "hbm_gbs",
                                      "exact_vs_raw")}
                   | {"x_raw": raw_step / r["step_ms"]} for r in results],

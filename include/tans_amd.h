@@ -41,6 +41,17 @@
  *     Streams start on 16-byte boundaries; 1 KiB of zero words follows the
  *     last one.  offsets is int64 [n_groups + 1], in words.
  *   - states[k] is lane k's initial decoder state in [L, 2L).
+ *   - Packed layout of short streams (pair alphabet, N <= 64, written by
+ *     tans_encode_packed_begin; a decoder is told by states == NULL): no
+ *     state array and no refill schedule.  Group g's stream at
+ *     comp_words[offsets[g] ..] is a header of 32 lane-pair bit counts
+ *     (u8 when N <= 16, else u16, little-endian) and a bit area after it
+ *     (bit b = bit b % 8 of its byte b / 8).  Pair p (lanes 2p, 2p + 1)
+ *     owns bits [S_p, E_p): S_p = the counts of pairs 0 .. p - 1 summed,
+ *     E_p = S_p + count p.  A lane's bits in decode order are (state - L)
+ *     in 12 bits, then each step's nb bits, each value LSB first; the even
+ *     lane's i-th bit is at S_p + i, the odd lane's at E_p - 1 - i.
+ *     Lanes past K count 0 bits.  Streams start on 16-byte boundaries.
  *   - Sign/mantissa nibbles: 16-element tiles, 8 bytes per (tile, lane) at
  *     sm[(t * K + k) * 8]; u32 word h covers elements 8h..8h+7 as
  *     (A & 0x87878787) | rotl(B & 0x87878787, 4), A/B being elements
@@ -111,6 +122,18 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S,
 int tans_encode_finish(void* handle, uint8_t* comp, uint16_t* states,
                        int64_t* offsets);
 void tans_encode_free(void* handle);
+
+/* tans_encode_begin into the packed layout of short streams (above):
+ * 2^12-state tables (the pair alphabet), 1 <= S <= 32 steps per lane.
+ * Same handle: tans_encode_finish writes comp and offsets and leaves
+ * states alone (it may be NULL; the layout has no state array).  Also
+ * replaces tans_encode_interleaved, csrc/tans_codec.cpp:69-196, for lanes
+ * of up to 64 FP8 bytes; the reference keeps one u16 state per stream
+ * (tans_codec.cpp:122-124) and pads each stream to whole u32 slabs.     */
+int tans_encode_packed_begin(const uint8_t* symbols, int64_t K, int64_t S,
+                             const int32_t* freqs, int32_t nsym, const int32_t* spread,
+                             int32_t log2L, void** handle, int64_t* comp_bytes,
+                             int64_t* n_offsets);
 
 /* Encode tables of (spread, freqs) for the GPU encoder: enc_tab [nsym] =
  * f_s | start_s << 16 (start_s = f_0 + ... + f_{s-1}), enc_next [2^log2L]

@@ -27,6 +27,10 @@
  *      derived from spread + freqs as rans_vectoradd/tans_codec.py:63-87),
  *      replayed over the wave-shared word stream, with the sign/mantissa nibbles
  *      unpacked bit by bit.  It shares no code with the product.
+ *   4. A checker for the packed layout of short streams (pair alphabet):
+ *      the same step semantics, each lane read bit by bit from its lane
+ *      pair's bits (forwards or backwards), with every count, final state
+ *      and padding bit checked.  Shares no code with the product either.
  */
 #include <math.h>
 #include <stdint.h>
@@ -527,6 +531,116 @@ int ora_w64_decode(const uint8_t* comp8, const int64_t* offsets, const uint16_t*
         for (int64_t p = pos; p < end && !bad; p++)
             if (comp[p]) bad = -14;
         for (int j = 0; j < 64; j++) free(ln[j].words);
+        if (bad) err = bad;
+    }
+    free(t_sym); free(t_nb); free(t_base);
+    return err;
+}
+
+/* ------------------------------------------------------------------ */
+/* 4. Checker for the packed layout of short streams                  */
+/* ------------------------------------------------------------------ */
+
+/* Layout being checked (written by the product encoder for the pair
+ * alphabet, L = 4096, at most 32 steps per lane):
+ *   group g's stream starts at byte 4*offsets[g]: 32 lane-pair bit counts
+ *   (1 byte each when N <= 16, else 2, little-endian), then a bit area
+ *   (bit b = bit b%8 of byte b/8 of the area).  Pair p = lanes 2p, 2p+1
+ *   owns bits [S_p, E_p), S_p = sum of the counts before p, E_p = S_p +
+ *   count_p.  A lane's bits in decode order: its initial state minus L
+ *   (12 bits), then each step's nb bits, every value LSB first.  The even
+ *   lane's i-th bit is at S_p + i, the odd lane's at E_p - 1 - i.  Lanes
+ *   past K count 0 bits; the rest of the stream is zero.
+ *   Sign/mantissa tiles as in section 3.
+ * Returns 0, or a negative code naming the first inconsistency: -11 final
+ * state != L, -12 a lane reads outside its pair's bits, -13 the pair's
+ * two lanes do not use its count exactly, -14 nonzero bits past the
+ * counts, -16 a lane past K with a nonzero count, -17 counts overrun the
+ * stream. */
+typedef struct {
+    const uint8_t* area;
+    int64_t lo, hi;     /* the pair's bits [lo, hi) */
+    int64_t at;         /* next bit (even: at, going up; odd: at - 1, going down) */
+    int dir;            /* +1 even lane, -1 odd lane */
+    int err;
+} pk_reader;
+
+static uint32_t pk_read(pk_reader* r, int nb)
+{
+    uint32_t v = 0;
+    for (int b = 0; b < nb; b++) {
+        int64_t pos = r->dir > 0 ? r->at : r->at - 1;
+        if (pos < r->lo || pos >= r->hi) { r->err = -12; return 0; }
+        v |= (uint32_t)((r->area[pos >> 3] >> (pos & 7)) & 1u) << b;
+        r->at += r->dir;
+    }
+    return v;
+}
+
+int ora_packed_decode(const uint8_t* comp8, const int64_t* offsets, const uint8_t* sm,
+                      const int32_t* spread, const int32_t* freqs, int64_t K, int64_t N,
+                      uint8_t* out /* [K, N] row-major */)
+{
+    const uint32_t L = 4096;
+    int32_t* t_sym = (int32_t*)malloc(sizeof(int32_t) * L);
+    int32_t* t_nb = (int32_t*)malloc(sizeof(int32_t) * L);
+    uint32_t* t_base = (uint32_t*)malloc(sizeof(uint32_t) * L);
+    int64_t* counts = (int64_t*)calloc(256, sizeof(int64_t));
+    for (uint32_t slot = 0; slot < L; slot++) {
+        int s = spread[slot];
+        uint32_t xp = (uint32_t)freqs[s] + (uint32_t)counts[s]++;
+        int nb = 0;
+        uint32_t v = xp;
+        while (v < L) { v <<= 1; nb++; }
+        t_sym[slot] = s; t_nb[slot] = nb; t_base[slot] = xp << nb;
+    }
+    free(counts);
+    const int64_t steps = N / 2;
+    const int hb = steps <= 8 ? 1 : 2;
+    const int64_t n_groups = (K + 63) / 64;
+    int err = 0;
+    #pragma omp parallel for schedule(dynamic, 4) reduction(min:err)
+    for (int64_t g = 0; g < n_groups; g++) {
+        const uint8_t* st = comp8 + offsets[g] * 4;
+        const int64_t bytes = (offsets[g + 1] - offsets[g]) * 4;
+        const int lanes = (int)((K - g * 64) < 64 ? (K - g * 64) : 64);
+        int bad = 0;
+        int64_t cnt[32], start[33];
+        start[0] = 0;
+        if (bytes < 32 * hb) bad = -17;
+        for (int p = 0; p < 32 && !bad; p++) {
+            cnt[p] = st[p * hb] | (hb == 2 ? (int64_t)st[p * hb + 1] << 8 : 0);
+            start[p + 1] = start[p] + cnt[p];
+            if (2 * p >= lanes && cnt[p]) bad = -16;
+        }
+        if (!bad && (start[32] + 7) / 8 > bytes - 32 * hb) bad = -17;
+        const uint8_t* area = st + 32 * hb;
+        for (int p = 0; p < 32 && !bad; p++) {
+            int64_t used = 0;
+            for (int side = 0; side < 2 && !bad; side++) {
+                const int j = 2 * p + side;
+                if (j >= lanes) continue;
+                const int64_t k = g * 64 + j;
+                pk_reader r = {area, start[p], start[p + 1], side ? start[p + 1] : start[p],
+                               side ? -1 : 1, 0};
+                uint32_t x = L + pk_read(&r, 12);
+                for (int64_t i = 0; i < steps && !r.err; i++) {
+                    uint32_t slot = x - L;
+                    int s = t_sym[slot];
+                    x = t_base[slot] + pk_read(&r, t_nb[slot]);
+                    const int64_t el = 2 * i;
+                    const uint8_t* sm8 = sm + ((el / 16) * K + k) * 8;
+                    out[k * N + el] = compose_fp8((uint32_t)(s >> 4), sm_nibble_of(sm8, (int)(el % 16)));
+                    out[k * N + el + 1] = compose_fp8((uint32_t)(s & 0xF), sm_nibble_of(sm8, (int)((el + 1) % 16)));
+                }
+                if (r.err) { bad = r.err; break; }
+                if (x != L) { bad = -11; break; }
+                used += side ? start[p + 1] - r.at : r.at - start[p];
+            }
+            if (!bad && used != cnt[p]) bad = -13;
+        }
+        for (int64_t b = start[32]; b < (bytes - 32 * hb) * 8 && !bad; b++)
+            if ((area[b >> 3] >> (b & 7)) & 1u) bad = -14;
         if (bad) err = bad;
     }
     free(t_sym); free(t_nb); free(t_base);

@@ -66,6 +66,8 @@ def lib() -> ctypes.CDLL:
         _lib.ora_ref_decode_add.argtypes = [P] * 12 + [I64, I64, P]
         _lib.ora_w64_decode.restype = I
         _lib.ora_w64_decode.argtypes = [P, P, P, P, P, P, I, I, I, I64, I64, P]
+        _lib.ora_packed_decode.restype = I
+        _lib.ora_packed_decode.argtypes = [P, P, P, P, P, I64, I64, P]
     return _lib
 
 
@@ -339,3 +341,29 @@ def w64_decode(comp, offsets, states, sm, spread, freqs, log2L: int, sps: int,
     if rc:
         raise ValueError(f"wave64 layout check failed ({rc})")
     return out
+
+
+# --------------------------------------------------------------------------
+# packed-layout checker (oracle.c section 4)
+# --------------------------------------------------------------------------
+
+def packed_decode(comp, offsets, sm, spread, freqs, K: int, N: int) -> np.ndarray:
+    """Decode the product's packed layout of short streams (pair alphabet)
+    on the CPU; returns [K, N].  Raises on any layout inconsistency."""
+    out = np.empty((K, N), np.uint8)
+    arrs = [np.ascontiguousarray(a) for a in (comp, offsets, sm)]
+    sp = np.ascontiguousarray(spread, dtype=np.int32)
+    fr = np.ascontiguousarray(freqs, dtype=np.int32)
+    rc = lib().ora_packed_decode(*[_p(a) for a in arrs], _p(sp), _p(fr), K, N, _p(out))
+    if rc:
+        raise ValueError(f"packed layout check failed ({rc})")
+    return out
+
+
+def layout_decode(enc, K: int, N: int, log2L: int = 12, sps: int = 2) -> np.ndarray:
+    """Decode an encode() 7-tuple of either layout (states empty: packed)."""
+    comp, states, offsets, _partial, sm, freqs, spread = (
+        t.numpy() if hasattr(t, "numpy") else t for t in enc)
+    if K and states.size == 0:
+        return packed_decode(comp, offsets, sm, spread, freqs, K, N)
+    return w64_decode(comp, offsets, states, sm, spread, freqs, log2L, sps, K, N)

@@ -126,9 +126,59 @@ int64_t encode_lane(const uint8_t* sym, int64_t S, const EncTables& t, uint32_t 
 
 struct EncodeHandle {
     int64_t K = 0, S = 0, n_groups = 0, total_words = 0;
+    bool packed = false;                          // packed layout: no states
     std::vector<std::vector<uint32_t>> streams;   // per group, 4-word padded
     std::vector<uint16_t> states;
 };
+
+// Bit writer of the packed layout's area (bit b = bit b % 8 of byte b / 8).
+inline void put_bit(uint8_t* area, int64_t b, uint32_t v) {
+    area[b >> 3] |= (uint8_t)((v & 1u) << (b & 7));
+}
+
+// One group of the packed layout (schedule.h, tans_pack): lanes' bits in
+// decode order are the state minus L and each step's chunk; even lanes
+// forwards from their pair's start, odd lanes backwards from its end.
+void pack_group(const uint32_t* chunk, const uint32_t* x0, int lanes, int64_t S, uint32_t L,
+                std::vector<uint32_t>& out) {
+    const int hb = tans_pack::hdr_bytes(S);
+    int64_t len[TANS_LANES] = {0};
+    for (int j = 0; j < lanes; j++) {
+        len[j] = tans_pack::kStateBits;
+        for (int64_t i = 0; i < S; i++) len[j] += (int64_t)(chunk[j * S + i] >> 16);
+    }
+    int64_t total = 0;
+    for (int j = 0; j < TANS_LANES; j++) total += len[j];
+    const int64_t bytes = (tans_pack::hdr_total(S) + (total + 7) / 8 + 15) / 16 * 16;
+    std::vector<uint8_t> buf((size_t)bytes, 0);
+    for (int p = 0; p < tans_pack::kPairs; p++) {
+        const uint32_t n = (uint32_t)(len[2 * p] + len[2 * p + 1]);
+        for (int b = 0; b < hb; b++) buf[(size_t)(p * hb + b)] = (uint8_t)(n >> (8 * b));
+    }
+    uint8_t* area = buf.data() + tans_pack::hdr_total(S);
+    int64_t start = 0;
+    for (int p = 0; p < tans_pack::kPairs; p++) {
+        const int64_t end = start + len[2 * p] + len[2 * p + 1];
+        for (int side = 0; side < 2; side++) {
+            const int j = 2 * p + side;
+            if (j >= lanes) break;
+            // bit i of the lane goes to start + i (even) or end - 1 - i (odd)
+            int64_t i = 0;
+            auto put = [&](uint32_t v, int nb) {
+                for (int b = 0; b < nb; b++, i++)
+                    put_bit(area, side ? end - 1 - i : start + i, v >> b);
+            };
+            put(x0[j] - L, tans_pack::kStateBits);
+            for (int64_t s = 0; s < S; s++) {
+                const uint32_t c = chunk[j * S + s];
+                put(c & 0xFFFFu, (int)(c >> 16));
+            }
+        }
+        start = end;
+    }
+    out.assign((size_t)(bytes / 4), 0u);
+    std::memcpy(out.data(), buf.data(), (size_t)bytes);
+}
 
 }  // namespace
 
@@ -216,15 +266,21 @@ int tans_build_encode_table(const int32_t* spread, const int32_t* freqs, int32_t
     return TANS_OK;
 }
 
-int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_t* freqs,
-                      int32_t nsym, const int32_t* spread, int32_t log2L, void** handle,
-                      int64_t* comp_bytes, int64_t* n_offsets) {
+}  // extern "C"
+
+namespace {
+
+int encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_t* freqs,
+                 int32_t nsym, const int32_t* spread, int32_t log2L, bool packed, void** handle,
+                 int64_t* comp_bytes, int64_t* n_offsets) {
     if (!handle || !comp_bytes || !n_offsets) return fail(TANS_EINVAL, "encode: null output");
     *handle = nullptr;
     if (K < 0 || S < 0 || (!symbols && K * S != 0) || !freqs || !spread)
         return fail(TANS_EINVAL, "encode: bad shape or null input");
     if (log2L < 1 || log2L > 12) return fail(TANS_EINVAL, "encode: log2L must be in [1, 12]");
     if (nsym < 1 || nsym > 256) return fail(TANS_EINVAL, "encode: nsym must be in [1, 256]");
+    if (packed && (log2L != TANS_PAIR_LOG2L || S < 1 || S > tans_pack::kMaxSteps))
+        return fail(TANS_EINVAL, "encode_packed: needs a 2^12-state table and 1..32 steps per lane");
     EncTables t;
     int rc = build_enc_tables(freqs, nsym, spread, log2L, t);
     if (rc) return rc;
@@ -233,6 +289,7 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
     if (!h) return fail(TANS_ENOMEM, "encode: out of memory");
     h->K = K;
     h->S = S;
+    h->packed = packed;
     h->n_groups = (K + TANS_LANES - 1) / TANS_LANES;
     try {
         h->streams.resize((size_t)h->n_groups);
@@ -249,6 +306,7 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
         std::vector<uint32_t> words((size_t)(TANS_LANES * max_words));
         std::vector<int64_t> nw(TANS_LANES), taken(TANS_LANES);
         std::vector<int32_t> cnt(TANS_LANES);
+        std::vector<uint32_t> x0s(TANS_LANES);
         #pragma omp for schedule(dynamic, 4)
         for (int64_t g = 0; g < h->n_groups; g++) {
             const int lanes = (int)std::min<int64_t>(TANS_LANES, K - g * TANS_LANES);
@@ -260,14 +318,19 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
                                     words.data() + j * max_words, &x0);
                 if (nw[j] < 0) { ok = false; break; }
                 h->states[(size_t)k] = (uint16_t)x0;
+                x0s[j] = x0;
             }
             if (!ok) {
                 #pragma omp atomic write
                 bad_symbol = 1;
                 continue;
             }
-            // Replay the decoders' refill schedule to order the words.
             std::vector<uint32_t>& out = h->streams[(size_t)g];
+            if (packed) {
+                pack_group(chunk.data(), x0s.data(), lanes, S, L, out);
+                continue;
+            }
+            // Replay the decoders' refill schedule to order the words.
             out.clear();
             out.reserve((size_t)(lanes * (max_words + 3)));
             auto take = [&](int j) {
@@ -308,9 +371,27 @@ int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_
     return TANS_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
+int tans_encode_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_t* freqs,
+                      int32_t nsym, const int32_t* spread, int32_t log2L, void** handle,
+                      int64_t* comp_bytes, int64_t* n_offsets) {
+    return encode_begin(symbols, K, S, freqs, nsym, spread, log2L, false, handle, comp_bytes,
+                        n_offsets);
+}
+
+int tans_encode_packed_begin(const uint8_t* symbols, int64_t K, int64_t S, const int32_t* freqs,
+                             int32_t nsym, const int32_t* spread, int32_t log2L, void** handle,
+                             int64_t* comp_bytes, int64_t* n_offsets) {
+    return encode_begin(symbols, K, S, freqs, nsym, spread, log2L, true, handle, comp_bytes,
+                        n_offsets);
+}
+
 int tans_encode_finish(void* handle, uint8_t* comp, uint16_t* states, int64_t* offsets) {
     EncodeHandle* h = static_cast<EncodeHandle*>(handle);
-    if (!h || !comp || !offsets || (!states && h->K)) {
+    if (!h || !comp || !offsets || (!states && h->K && !h->packed)) {
         delete h;
         return fail(TANS_EINVAL, "encode_finish: null argument");
     }
@@ -327,7 +408,7 @@ int tans_encode_finish(void* handle, uint8_t* comp, uint16_t* states, int64_t* o
         if (!st.empty()) std::memcpy(c32 + offsets[g], st.data(), st.size() * 4);
     }
     std::memset(c32 + cum, 0, (size_t)kTailWords * 4);
-    if (h->K) std::memcpy(states, h->states.data(), (size_t)h->K * 2);
+    if (h->K && !h->packed) std::memcpy(states, h->states.data(), (size_t)h->K * 2);
     delete h;
     return TANS_OK;
 }

@@ -627,7 +627,10 @@ __device__ __forceinline__ void table_fetch(TableRegs<L>& r, const v2u* __restri
     for (uint32_t k = 0; k < L / kDecBlock; k++) r.e[k] = table[threadIdx.x + k * kDecBlock];
 }
 
-template <uint32_t L>
+// PACKED: the entries of the packed-layout decoders, whose word0 keeps nb
+// in bits 4:0 and moves the two exponents 8 bits up (bits 22:19 and
+// 30:27), so that bits 15:0 of a sum of word0s are the sum of their nb.
+template <uint32_t L, bool PACKED = false>
 __device__ __forceinline__ void table_store(v2u* lds, const TableRegs<L>& r) {
     constexpr uint32_t log2L = 31 - __builtin_clz(L);
     constexpr uint32_t max_nb =
@@ -639,7 +642,185 @@ __device__ __forceinline__ void table_store(v2u* lds, const TableRegs<L>& r) {
         const uint32_t base = e.y >> 3;
         if (nb > max_nb || (e.x >> 27) != nb || (e.y & 7u) || base + (1u << nb) > L)
             e = v2u{e.x & 0x07FFFF00u, 0u};
+        if constexpr (PACKED) e.x = (e.x & 0x1Fu) | ((e.x & 0x007FF800u) << 8);
         lds[threadIdx.x + k * kDecBlock] = e;
+    }
+}
+
+// ---------------------------------------------------------------------
+// Packed layout of short streams (include/tans_amd.h; schedule.h,
+// tans_pack): pair alphabet, at most four 16-element tiles per lane.  A
+// wave loads a group's whole stream (header of lane-pair bit counts, then
+// the bit area) into its ring region with 16-byte loads, scans the counts
+// once, and from then on each lane reads its own bits at a cursor: there
+// is no shared word stream, no refill and no state array.  Even lanes read
+// forwards from their pair's start, odd lanes backwards from its end.  Per
+// two steps a lane takes the 32 bits at its cursor (one ds_read2_b32 and a
+// funnel shift; odd lanes reverse them with v_bfrev), extracts the two
+// fields as the streaming decoder does, and advances the cursor by nb1 +
+// nb2 with one add of the two entries' word0 (table_store<L, true>).
+// Kernels select it with FIRST = -(tiles per lane).
+// ---------------------------------------------------------------------
+constexpr int kPackRegionBytes = kRingAlloc * 4;
+constexpr int kPackMaxSegs = 4;                 // 16-byte loads per lane for 4 tiles
+static_assert(tans_pack::max_stream_bytes(tans_pack::kMaxSteps) + 8 <= kPackRegionBytes &&
+                  kPackRegionBytes <= kPackMaxSegs * kSegWords * 4,
+              "a packed stream of four tiles fits the ring region with 8 bytes to spare");
+
+// Segment loads that cover a packed stream of NT tiles (8 NT pair steps).
+__host__ __device__ constexpr int pack_segs(int NT) {
+    return (int)((tans_pack::max_stream_bytes(8 * NT) + kSegWords * 4 - 1) / (kSegWords * 4));
+}
+
+// Odd lanes of the wave (the backward half of each lane pair).
+constexpr Mask kOddLanes = 0xAAAAAAAAAAAAAAAAull;
+
+struct PLane {
+    uint32_t a;       // the window's start at c = 0: the pair start (even lanes),
+                      // the pair end - 64 (odd lanes)
+    uint32_t sgn;     // 1 (even lanes) or 0xFFFF (odd lanes)
+    uint32_t c;       // bits 15:0 the lane's bits read so far; the bits above collect exponents
+    uint32_t x8;      // (state - L) * 8
+    uint32_t lo, hi;  // the first window of a stream (pk_start): 64 bits in decode order
+};
+
+// The 64 bits at the lane's cursor in decode order, as (hi:lo): area bits
+// [p, p + 64) with p = a + c (even lanes), or a - c (odd lanes, whose bits
+// run backwards: both words reversed and swapped), p taken mod 2^16 by
+// v_mad_u32_u16 (c.u16 * sgn.u16 + a).  Three LDS words per lane.
+__device__ __forceinline__ void pk_window(const PLane& l, const uint32_t* region, uint32_t& lo,
+                                          uint32_t& hi) {
+    uint32_t pos;
+    asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(pos) : "v"(l.c), "v"(l.sgn), "v"(l.a));
+    const uint32_t idx = __builtin_amdgcn_ubfe(pos, 5u, 11u);
+    const uint32_t d0 = region[idx], d1 = region[idx + 1], d2 = region[idx + 2];
+    const uint32_t w0 = __builtin_amdgcn_alignbit(d1, d0, pos);
+    const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1, pos);
+    lo = select(kOddLanes, __builtin_bitreverse32(w1), w0);
+    hi = select(kOddLanes, __builtin_bitreverse32(w0), w1);
+}
+
+// Two tANS steps from the 32 bits t; w1/w2 get the entries' word0.
+__device__ __forceinline__ void pk_steps(PLane& l, uint32_t t, const v2u* __restrict__ tbl,
+                                         uint32_t& w1, uint32_t& w2) {
+    const v2u e1 = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
+    const uint32_t b1 = __builtin_amdgcn_ubfe(t, 0u, e1.x);
+    l.x8 = (b1 << 3) + e1.y;
+    const v2u e2 = *reinterpret_cast<const v2u*>(reinterpret_cast<const char*>(tbl) + l.x8);
+    const uint32_t b2 = __builtin_amdgcn_ubfe(t, e1.x, e2.x);
+    l.x8 = (b2 << 3) + e2.y;
+    w1 = e1.x;
+    w2 = e2.x;
+}
+
+// A group's packed stream (words s .. e of comp, clamped to the buffer):
+// NSEG 16-byte loads per lane, zeros past the stream.  Returns its bytes.
+template <int NSEG>
+__device__ __forceinline__ uint32_t pk_fetch(const uint32_t* comp, int64_t words, int64_t s,
+                                             int64_t e, int lane, Seg (&seg)[kPackMaxSegs]) {
+    s = s < 0 ? 0 : (s > words ? words : s);
+    e = e < s ? s : (e > words ? words : e);
+    const int64_t room = (words - s) * 4;
+    const uint32_t bound = room > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)room;
+    const int64_t len = (e - s) * 4;
+    const uint32_t len_b = len > (int64_t)bound ? bound : (uint32_t)len;
+    const Rsrc src = rsrc(comp + s, bound);
+    #pragma unroll
+    for (int i = 0; i < NSEG; i++) {
+        const uint32_t b = (uint32_t)(i * kSegWords * 4);
+        seg[i] = __builtin_amdgcn_raw_buffer_load_b128(src, b < len_b ? (uint32_t)lane * 16u + b
+                                                                      : kNoSeg, 0, 0);
+    }
+    return len_b;
+}
+
+// Inclusive sum over the wave's lanes (DPP: four row shifts within each row
+// of 16 lanes, then two row broadcasts across rows).
+__device__ __forceinline__ uint32_t wave_scan(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, true);   // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, true);   // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, true);   // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, true);   // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return v;
+}
+
+// Write the stream into the wave's region (the fourth load only up to the
+// region's end), read the header, set up the lane's cursor and take its
+// first window: the state (12 bits) and the first two segments.  The
+// wave's LDS accesses execute in order, so its reads see its writes.
+// Cursors are clamped so that 8 NT steps (at most T bits) and the 96-bit
+// read stay inside the region whatever the header says; a well-formed
+// stream never meets the clamp.
+template <int NT, int NSEG>
+__device__ __forceinline__ void pk_start(PLane& l, uint32_t* region, int lane,
+                                         const Seg (&seg)[kPackMaxSegs], uint32_t len_b) {
+    // (compiler barriers: the region is written as 16-byte vectors and read
+    // as words, which type-based alias analysis would let it reorder)
+    asm volatile("" ::: "memory");
+    #pragma unroll
+    for (int i = 0; i < NSEG; i++)
+        if ((i == 0 || (uint32_t)(i * kSegWords * 4) < len_b) &&
+            ((i + 1) * kSegWords * 4 <= kPackRegionBytes ||
+             lane * 16 < kPackRegionBytes - i * kSegWords * 4))
+            reinterpret_cast<Seg*>(region + i * kSegWords)[lane] = seg[i];
+    asm volatile("" ::: "memory");
+    constexpr int hb = NT == 1 ? 1 : 2;   // tans_pack::hdr_bytes(8 NT)
+    static_assert(hb == tans_pack::hdr_bytes(8 * NT) && hb == tans_pack::hdr_bytes(8 * NT - 7),
+                  "one header width for every stream length of NT tiles");
+    const uint32_t hbyte = (uint32_t)(lane >> 1) * hb;   // the pair's count in the header
+    const uint32_t cnt = (region[hbyte >> 2] >> (8 * (hbyte & 3))) & (hb == 1 ? 0xFFu : 0xFFFFu);
+    // the pair's end: the counts of even lanes summed up to this lane
+    const uint32_t end = (uint32_t)tans_pack::hdr_total(8 * NT) * 8u +
+                         wave_scan((lane & 1) ? 0u : cnt);
+    constexpr uint32_t T = (uint32_t)tans_pack::max_lane_bits(8 * NT);
+    constexpr uint32_t R = kPackRegionBytes * 8;
+    if (lane & 1) {
+        const uint32_t a = end - 64u;
+        l.a = a < T ? T : (a > R - 96u ? R - 96u : a);
+        l.sgn = 0xFFFFu;
+    } else {
+        const uint32_t a = end - cnt;
+        l.a = a > R - 96u - T ? R - 96u - T : a;
+        l.sgn = 1u;
+    }
+    l.c = 0u;
+    pk_window(l, region, l.lo, l.hi);
+    l.x8 = (l.lo & 0xFFFu) << 3;
+}
+
+// The 16 elements of one tile of every chain (4 exponent words each): two
+// windows of two segments each.  START: the stream's first tile, whose
+// first window is pk_start's, after the 12 bits of the state.
+template <int C, bool START>
+__device__ __forceinline__ void pk_tile(PLane (&l)[C], uint32_t* const (&region)[C],
+                                        const v2u* __restrict__ tbl, uint32_t (&ex)[C][4]) {
+    #pragma unroll
+    for (int h = 0; h < 2; h++) {
+        #pragma unroll
+        for (int c = 0; c < C; c++) {
+            uint32_t lo, hi, off = 0, w1, w2, w3, w4;
+            if (START && h == 0) {
+                lo = l[c].lo;
+                hi = l[c].hi;
+                off = (uint32_t)tans_pack::kStateBits;
+            } else {
+                pk_window(l[c], region[c], lo, hi);
+            }
+            pk_steps(l[c], __builtin_amdgcn_alignbit(hi, lo, off), tbl, w1, w2);
+            const uint32_t s12 = off + w1 + w2;   // bits 15:0: off + nb1 + nb2
+            uint32_t t2;
+            if (START && h == 0) {   // 12 + nb1 + nb2 can reach 36: a 64-bit shift
+                t2 = (uint32_t)((((uint64_t)hi << 32) | lo) >> (s12 & 63u));
+            } else {                 // nb1 + nb2 <= 24
+                t2 = __builtin_amdgcn_alignbit(hi, lo, s12);
+            }
+            pk_steps(l[c], t2, tbl, w3, w4);
+            l[c].c += s12 + w3 + w4;
+            ex[c][2 * h] = __builtin_amdgcn_perm(w2, w1, 0x07060302u);       // bytes 2, 3 of each
+            ex[c][2 * h + 1] = __builtin_amdgcn_perm(w4, w3, 0x07060302u);
+        }
     }
 }
 
@@ -804,11 +985,15 @@ __device__ __forceinline__ void dec_tile(Chains<C>& ch, const v2u* __restrict__ 
 // FIRST > 0: every stream fits FIRST ring segments and is loaded whole at
 // its start, with its (at most kSmAhead) sign/mantissa tiles: no stage
 // fetches, no sign/mantissa prefetch.  FIRST = 0: streams of any length.
+// FIRST < 0: the packed layout, -FIRST tiles per lane, loaded whole too.
 template <int SPS, int G, int FIRST>
 struct FusedWave {
-    static constexpr bool RES = FIRST > 0;
+    static constexpr bool PACKED = FIRST < 0;
+    static constexpr bool RES = FIRST != 0;
     static constexpr int C = 2 * G;   // chain 2g: A of group g, 2g + 1: B of group g
     Chains<C> ch;
+    PLane pk[C];            // packed layout: the lanes' cursors
+    uint32_t* preg[C];      // packed layout: each chain's stream region (LDS)
     v2u sm[C][kSmAhead];    // sign/mantissa words of tiles t .. t + kSmAhead - 1 (by t mod kSmAhead)
     const char* pf[C];      // sign/mantissa row of the next prefetch (wave-uniform)
     char* out_cur[G];       // output row of the current tile (wave-uniform)
@@ -826,7 +1011,8 @@ struct FusedWave {
     template <int P, bool LAST>
     __device__ __forceinline__ void tile(int t) {
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST, RES>(ch, tbl, lane, ex);
+        if constexpr (PACKED) pk_tile<C, P == 0>(pk, preg, tbl, ex);
+        else dec_tile<SPS, C, LAST, RES>(ch, tbl, lane, ex);
         pace(progress, lane, (uint32_t)(base + t), live);
         #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -884,10 +1070,14 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     int64_t g0 = ((int64_t)blockIdx.x * kDecWaves + wave) * G;
     const bool live = g0 < n_groups;   // wave-uniform
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * G;
-    constexpr int NSEG = FIRST > 0 ? FIRST : kSlots;   // segments loaded at a start
-    constexpr int NSM = FIRST == Alpha<SPS>::kOneTileSegs ? 1 : kSmAhead;   // sm tiles loaded then
-    static_assert(FIRST == 0 || FIRST == Alpha<SPS>::kOneTileSegs || FIRST == kSlots,
-                  "one-tile streams, streams of up to kResidentTiles tiles, or any");
+    constexpr bool PACKED = FIRST < 0;
+    // segments loaded at a start, and sign/mantissa tiles loaded then
+    constexpr int NSEG = FIRST > 0 ? FIRST : PACKED ? pack_segs(-FIRST) : kSlots;
+    constexpr int NSM = PACKED ? -FIRST : FIRST == Alpha<SPS>::kOneTileSegs ? 1 : kSmAhead;
+    static_assert(FIRST == 0 || FIRST == Alpha<SPS>::kOneTileSegs || FIRST == kSlots ||
+                      (PACKED && SPS == 2 && -FIRST <= kSmAhead),
+                  "one-tile streams, streams of up to kResidentTiles tiles, any streams, or "
+                  "packed streams of up to 4 tiles");
     static_assert(Alpha<SPS>::kResidentTiles <= kSmAhead,
                   "a resident stream's sign/mantissa tiles are all loaded at its start");
     FusedWave<SPS, G, FIRST> w;
@@ -898,16 +1088,19 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     w.tbl = tbl;
     w.sm_stride = K * 8;
     w.out_stride = K * 16;
-    Seg first[C][kSlots];
+    Seg first[C][PACKED ? kPackMaxSegs : kSlots];
     uint16_t st0[C];
+    uint32_t plen[C];   // packed layout: bytes of each chain's stream
     int glanes[G];
+    #pragma unroll
+    for (int c = 0; c < C; c++) w.preg[c] = smem.rings[wave][c];
     // the loads of the groups gbase .. gbase + G - 1
     // With resident streams a wave switches groups every few tiles, and the
     // switch waits on the next group's stream offsets: they are loaded
     // during the last tile instead, by lanes 0-3 (a vector load, so the
     // tile's own waits do not include it), and read with v_readlane.
     // (not in the nibble kernel for two-tile streams: it has no VGPRs to spare)
-    constexpr bool AHEAD = FIRST > 0 && (SPS == 2 || FIRST == Alpha<SPS>::kOneTileSegs);
+    constexpr bool AHEAD = PACKED || (FIRST > 0 && (SPS == 2 || FIRST == Alpha<SPS>::kOneTileSegs));
     static_assert(G == 1 || !AHEAD, "offsets ahead for one group per wave");
     int64_t noff = 0;
     auto next_offsets = [&](int64_t gnext) {
@@ -936,12 +1129,17 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             } else {
                 sa = a_off[g]; ea = a_off[g + 1]; sb = b_off[g]; eb = b_off[g + 1];
             }
-            feed_fetch<NSEG>(w.ch.f[2 * j], a_comp, a_words, sa, ea, smem.rings[wave][2 * j],
-                             tbl, lane, first[2 * j]);
-            feed_fetch<NSEG>(w.ch.f[2 * j + 1], b_comp, b_words, sb, eb,
-                             smem.rings[wave][2 * j + 1], tbl, lane, first[2 * j + 1]);
-            st0[2 * j] = a_st[k0 + lane_ld];
-            st0[2 * j + 1] = b_st[k0 + lane_ld];
+            if constexpr (PACKED) {
+                plen[2 * j] = pk_fetch<NSEG>(a_comp, a_words, sa, ea, lane, first[2 * j]);
+                plen[2 * j + 1] = pk_fetch<NSEG>(b_comp, b_words, sb, eb, lane, first[2 * j + 1]);
+            } else {
+                feed_fetch<NSEG>(w.ch.f[2 * j], a_comp, a_words, sa, ea, smem.rings[wave][2 * j],
+                                 tbl, lane, first[2 * j]);
+                feed_fetch<NSEG>(w.ch.f[2 * j + 1], b_comp, b_words, sb, eb,
+                                 smem.rings[wave][2 * j + 1], tbl, lane, first[2 * j + 1]);
+                st0[2 * j] = a_st[k0 + lane_ld];
+                st0[2 * j + 1] = b_st[k0 + lane_ld];
+            }
             glanes[j] = lanes;
             const char* rows[2] = {reinterpret_cast<const char*>(a_sm + k0),
                                    reinterpret_cast<const char*>(b_sm + k0)};
@@ -961,7 +1159,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
         }
     };
     setup(g0, false);
-    table_store<L>(tbl, tr);
+    table_store<L, PACKED>(tbl, tr);
     if (threadIdx.x == 0) smem.init();
     __syncthreads();
     if (!live) return;
@@ -969,8 +1167,12 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     for (;;) {
         #pragma unroll
         for (int c = 0; c < C; c++) {
-            feed_commit<NSEG>(w.ch.f[c], lane, first[c], w.ch.p[c]);
-            lane_init(w.ch.l[c], w.ch.f[c], lane, glanes[c / 2], st0[c], L, smem.sink_off());
+            if constexpr (PACKED) {
+                pk_start<-FIRST, NSEG>(w.pk[c], w.preg[c], lane, first[c], plen[c]);
+            } else {
+                feed_commit<NSEG>(w.ch.f[c], lane, first[c], w.ch.p[c]);
+                lane_init(w.ch.l[c], w.ch.f[c], lane, glanes[c / 2], st0[c], L, smem.sink_off());
+            }
         }
         w.base = done;
         // the first n_tiles - 1 tiles four per iteration, then the last one,
@@ -1049,12 +1251,16 @@ struct DecodeSmem {
 static_assert(sizeof(DecodeSmem<2>) <= 160 * 1024 && sizeof(DecodeSmem<1>) <= 160 * 1024,
               "decoder LDS exceeds the 160 KiB of a gfx950 CU");
 
-// FIRST as in FusedWave: > 0 for streams loaded whole at their start.
+// FIRST as in FusedWave: > 0 for streams loaded whole at their start,
+// < 0 for the packed layout.
 template <int SPS, int FIRST>
 struct DecodeWave {
     static constexpr int C = kDecodeGroups;
-    static constexpr bool RES = FIRST > 0;
+    static constexpr bool PACKED = FIRST < 0;
+    static constexpr bool RES = FIRST != 0;
     Chains<C> ch;
+    PLane pk[C];            // packed layout: the lanes' cursors
+    uint32_t* preg[C];      // packed layout: each group's stream region (LDS)
     v2u sm[C][kSmAhead];    // sign/mantissa words of tiles t .. t + kSmAhead - 1 (by t mod kSmAhead)
     const char* pf[C];      // sign/mantissa row of the next prefetch (wave-uniform)
     uint32_t sm_bytes[C];   // bytes of a group's sm row (8 per lane in range)
@@ -1084,7 +1290,8 @@ struct DecodeWave {
         // symbol come after every real one (no refill checks there), stay
         // inside the table, and their bytes are not stored.
         uint32_t ex[C][4];
-        dec_tile<SPS, C, LAST, RES>(ch, tbl, lane, ex, last_segs, fin_pos);
+        if constexpr (PACKED) pk_tile<C, P == 0>(pk, preg, tbl, ex);
+        else dec_tile<SPS, C, LAST, RES>(ch, tbl, lane, ex, last_segs, fin_pos);
         pace(progress, lane, (uint32_t)(base + t), live);
         uint32_t w[C][4];
         #pragma unroll
@@ -1204,10 +1411,13 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     const int64_t wg_groups = n_groups - (int64_t)blockIdx.x * kDecWaves * C;
     // as in fused_add_kernel (a lazy start measured within noise here:
     // 2^30 elements at 1024 per lane -0.3%, at 128 per lane +0.6%)
-    constexpr int NSEG = FIRST > 0 ? FIRST : kSlots;
-    constexpr int NSM = FIRST == Alpha<SPS>::kOneTileSegs ? 1 : kSmAhead;
-    static_assert(FIRST == 0 || FIRST == Alpha<SPS>::kOneTileSegs || FIRST == kSlots,
-                  "one-tile streams, streams of up to kResidentTiles tiles, or any");
+    constexpr bool PACKED = FIRST < 0;
+    constexpr int NSEG = FIRST > 0 ? FIRST : PACKED ? pack_segs(-FIRST) : kSlots;
+    constexpr int NSM = PACKED ? -FIRST : FIRST == Alpha<SPS>::kOneTileSegs ? 1 : kSmAhead;
+    static_assert(FIRST == 0 || FIRST == Alpha<SPS>::kOneTileSegs || FIRST == kSlots ||
+                      (PACKED && SPS == 2 && -FIRST <= kSmAhead),
+                  "one-tile streams, streams of up to kResidentTiles tiles, any streams, or "
+                  "packed streams of up to 4 tiles");
     DecodeWave<SPS, FIRST> w;
     w.progress = &smem.progress;
     w.live = (uint32_t)(wg_groups >= (int64_t)kDecWaves * C ? kDecWaves : (wg_groups + C - 1) / C);
@@ -1222,8 +1432,11 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     quad_selectors(lane, w.sel1, w.sel2);
     w.xp = dsmem.xpose[wave];
     w.lines = K % 16 == 0;
-    Seg first[C][kSlots];
+    Seg first[C][PACKED ? kPackMaxSegs : kSlots];
     uint16_t st0[C];
+    uint32_t plen[C];   // packed layout: bytes of each group's stream
+    #pragma unroll
+    for (int j = 0; j < C; j++) w.preg[j] = smem.rings[wave][j];
     // the loads of the groups gbase, gbase + 1
     auto setup = [&](int64_t gbase) {
         bool full = true;
@@ -1246,9 +1459,13 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
             const bool active = lane < lanes;
             const uint32_t lane_ld = (uint32_t)(active ? lane : (lanes ? lanes - 1 : 0));
             w.sm_bytes[j] = (uint32_t)lanes * 8u;
-            feed_fetch<NSEG>(w.ch.f[j], comp, words, os[j], oe[j], smem.rings[wave][j], tbl,
-                             lane, first[j]);
-            st0[j] = st[k0 + lane_ld];
+            if constexpr (PACKED) {
+                plen[j] = pk_fetch<NSEG>(comp, words, os[j], oe[j], lane, first[j]);
+            } else {
+                feed_fetch<NSEG>(w.ch.f[j], comp, words, os[j], oe[j], smem.rings[wave][j], tbl,
+                                 lane, first[j]);
+                st0[j] = st[k0 + lane_ld];
+            }
             const char* row = reinterpret_cast<const char*>(sm + k0);
             #pragma unroll
             for (int i = 0; i < NSM; i++) {
@@ -1263,7 +1480,7 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
         w.full = full;
     };
     setup(g0);
-    table_store<L>(tbl, tr);
+    table_store<L, PACKED>(tbl, tr);
     if (threadIdx.x == 0) smem.init();
     __syncthreads();
     if (!live) return;
@@ -1271,8 +1488,12 @@ __global__ __launch_bounds__(kDecBlock) void decode_kernel(
     for (;;) {
         #pragma unroll
         for (int j = 0; j < C; j++) {
-            feed_commit<NSEG>(w.ch.f[j], lane, first[j], w.ch.p[j]);
-            lane_init(w.ch.l[j], w.ch.f[j], lane, w.lanes[j], st0[j], L, smem.sink_off());
+            if constexpr (PACKED) {
+                pk_start<-FIRST, NSEG>(w.pk[j], w.preg[j], lane, first[j], plen[j]);
+            } else {
+                feed_commit<NSEG>(w.ch.f[j], lane, first[j], w.ch.p[j]);
+                lane_init(w.ch.l[j], w.ch.f[j], lane, w.lanes[j], st0[j], L, smem.sink_off());
+            }
         }
         w.base = done;
         w.run(rag ? rag : kTile);
@@ -1978,9 +2199,15 @@ int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes, const int64_
     if (!sps) return fail(TANS_EINVAL, "vecadd_fused: log2L must be 12 (pair) or 11 (nibble)");
     if (K < 0 || N < 0 || N % kTile) return fail(TANS_EINVAL, "vecadd_fused: N must be a multiple of 16");
     if (K == 0 || N == 0) return TANS_OK;
-    if (!a_comp || !a_offsets || !a_states || !a_sm || !b_comp || !b_offsets || !b_states || !b_sm ||
-        !table || !out)
+    if (!a_comp || !a_offsets || !a_sm || !b_comp || !b_offsets || !b_sm || !table || !out)
         return fail(TANS_EINVAL, "vecadd_fused: null pointer");
+    // no state arrays: the packed layout of short streams
+    const bool packed = !a_states;
+    if (packed != !b_states)
+        return fail(TANS_EINVAL, "vecadd_fused: A and B must both have states or both be packed");
+    if (packed && (sps != 2 || N > 16 * kPackMaxSegs))
+        return fail(TANS_EINVAL, "vecadd_fused: the packed layout needs the pair table (log2L 12) "
+                                 "and N <= 64");
     if (a_comp_bytes < 0 || b_comp_bytes < 0 || a_comp_bytes % 4 || b_comp_bytes % 4)
         return fail(TANS_EINVAL, "vecadd_fused: compressed sizes must be multiples of 4 bytes");
     if (!aligned(a_comp, 16) || !aligned(b_comp, 16) || !aligned(a_sm, 8) || !aligned(b_sm, 8) ||
@@ -2002,7 +2229,14 @@ int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes, const int64_
                        (const uint32_t*)b_comp, b_comp_bytes / 4, b_offsets, b_states,           \
                        (const v2u*)b_sm, (const v2u*)table, K, n_tiles, (v4u*)out)
     // streams that fit the ring are loaded whole at their start
-    if (sps == 2) {
+    if (packed) {
+        switch (n_tiles) {
+            case 1: TANS_LAUNCH_FUSED(2, -1); break;
+            case 2: TANS_LAUNCH_FUSED(2, -2); break;
+            case 3: TANS_LAUNCH_FUSED(2, -3); break;
+            default: TANS_LAUNCH_FUSED(2, -4); break;
+        }
+    } else if (sps == 2) {
         if (n_tiles == 1) TANS_LAUNCH_FUSED(2, Alpha<2>::kOneTileSegs);
         else if (n_tiles <= Alpha<2>::kResidentTiles) TANS_LAUNCH_FUSED(2, kSlots);
         else TANS_LAUNCH_FUSED(2, 0);
@@ -2022,8 +2256,13 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
     if (!sps) return fail(TANS_EINVAL, "decode: log2L must be 12 (pair) or 11 (nibble)");
     if (K < 0 || N < 0 || N % 2) return fail(TANS_EINVAL, "decode: N must be even");
     if (K == 0 || N == 0) return TANS_OK;
-    if (!comp || !offsets || !states || !sm || !table || !out)
+    if (!comp || !offsets || !sm || !table || !out)
         return fail(TANS_EINVAL, "decode: null pointer");
+    // no state array: the packed layout of short streams
+    const bool packed = !states;
+    if (packed && (sps != 2 || N > 16 * kPackMaxSegs))
+        return fail(TANS_EINVAL, "decode: the packed layout needs the pair table (log2L 12) and "
+                                 "N <= 64");
     if (comp_bytes < 0 || comp_bytes % 4)
         return fail(TANS_EINVAL, "decode: compressed size must be a multiple of 4 bytes");
     if (!aligned(comp, 16) || !aligned(sm, 8) || !aligned(offsets, 8) || !aligned(states, 2) ||
@@ -2052,7 +2291,14 @@ int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
                        (uint8_t*)out)
     // streams that fit the ring are loaded whole at their start
     const int64_t n_tiles = (N + kTile - 1) / kTile;
-    if (sps == 2) {
+    if (packed) {
+        switch (n_tiles) {
+            case 1: TANS_LAUNCH_DECODE(2, -1); break;
+            case 2: TANS_LAUNCH_DECODE(2, -2); break;
+            case 3: TANS_LAUNCH_DECODE(2, -3); break;
+            default: TANS_LAUNCH_DECODE(2, -4); break;
+        }
+    } else if (sps == 2) {
         if (n_tiles == 1) TANS_LAUNCH_DECODE(2, Alpha<2>::kOneTileSegs);
         else if (n_tiles <= Alpha<2>::kResidentTiles) TANS_LAUNCH_DECODE(2, kSlots);
         else TANS_LAUNCH_DECODE(2, 0);

@@ -21,9 +21,9 @@
 #include <stdint.h>
 
 #ifdef __HIPCC__
-#define TANS_SCHED_FN __host__ __device__ __forceinline__
+#define TANS_SCHED_FN constexpr __host__ __device__ __forceinline__
 #else
-#define TANS_SCHED_FN inline
+#define TANS_SCHED_FN constexpr
 #endif
 
 namespace tans_sched {
@@ -100,5 +100,38 @@ TANS_SCHED_FN int decoder_below(int64_t S, bool triple, int64_t j) {
 }
 
 }  // namespace tans_sched
+
+// The packed layout of short streams (pair alphabet, at most kMaxSteps
+// steps per lane), shared by the CPU encoder and the decoders.  A group's
+// stream is a header of kPairs lane-pair bit counts (hdr_bytes each) and a
+// bit area right after it.  Lane pair p = lanes 2p, 2p + 1 owns bits
+// [S_p, E_p) of the area, S_p = the counts of the pairs before it summed,
+// E_p = S_p + count p.  A lane's bits in decode order are its initial
+// state minus L (kStateBits) and then each step's nb bits, LSB first; the
+// even lane's go forwards from S_p (its i-th bit at S_p + i), the odd
+// lane's backwards from E_p (its i-th bit at E_p - 1 - i).  Bit b of the
+// area is bit b % 8 of its byte b / 8.  No refill schedule: a decoder keeps
+// one bit cursor per lane.  The stream is padded with zeros to 16 bytes.
+namespace tans_pack {
+
+constexpr int kPairs = 32;          // lane pairs of a 64-lane group
+constexpr int kStateBits = 12;      // the state minus L, 2^12-state tables
+constexpr int kMaxNb = 12;
+constexpr int64_t kMaxSteps = 32;   // 64 elements per lane (four 16-element tiles)
+
+// Header entry bytes: one while a pair's bits fit (8 steps: at most
+// 2 * (12 + 8 * 12) = 216), else two.
+TANS_SCHED_FN int hdr_bytes(int64_t S) { return S <= 8 ? 1 : 2; }
+TANS_SCHED_FN int hdr_total(int64_t S) { return kPairs * hdr_bytes(S); }
+
+// The most bits one lane can hold for S steps.
+TANS_SCHED_FN int64_t max_lane_bits(int64_t S) { return kStateBits + (int64_t)kMaxNb * S; }
+
+// The most bytes a group's stream can take (header, area, padding to 16).
+TANS_SCHED_FN int64_t max_stream_bytes(int64_t S) {
+    return (hdr_total(S) + (2 * kPairs * max_lane_bits(S) + 7) / 8 + 15) / 16 * 16;
+}
+
+}  // namespace tans_pack
 
 #endif  // TANS_SCHEDULE_H

@@ -22,8 +22,8 @@ import ctypes
 
 import torch
 
-from ._lib import (TANS_GEMM_MAX_BATCH, TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PAIR_LOG2L,
-                   TANS_TILE, check, lib)
+from ._lib import (TANS_GEMM_MAX_BATCH, TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PACKED_MAX_N,
+                   TANS_PAIR_LOG2L, TANS_TILE, check, lib)
 
 __all__ = [
     "tans_encode_interleaved",
@@ -78,12 +78,15 @@ def log2_states(n: int) -> int:
 
 
 def tans_encode_interleaved(symbols: torch.Tensor, freqs: torch.Tensor,
-                            spread: torch.Tensor):
+                            spread: torch.Tensor, *, packed: bool = False):
     """CPU tANS encoder -> wave64 lane layout.  (csrc/tans_codec.cpp:69-196)
 
     symbols [K, S] uint8 (one symbol per decode step), freqs int32 summing to
     L = spread.numel(), spread [L] int32.  Returns (compressed uint8,
-    states uint16 [K], offsets int64 [ceil(K/64)+1], partial uint8 [0])."""
+    states uint16 [K], offsets int64 [ceil(K/64)+1], partial uint8 [0]).
+    ``packed`` (a keyword the reference does not have) writes the packed
+    layout of short streams instead (2^12-state tables, S <= 32): the
+    initial states go into the streams and ``states`` comes back empty."""
     _require(symbols.dim() == 2, "symbols must be [K, N]")
     _check_cpu("symbols", symbols, torch.uint8)
     _check_cpu("freqs", freqs, torch.int32)
@@ -94,13 +97,14 @@ def tans_encode_interleaved(symbols: torch.Tensor, freqs: torch.Tensor,
     handle = ctypes.c_void_p()
     comp_bytes = ctypes.c_int64()
     n_off = ctypes.c_int64()
-    check(lib.tans_encode_begin(_ptr(symbols), K, S, _ptr(freqs), freqs.numel(), _ptr(spread),
-                                L.bit_length() - 1, ctypes.byref(handle),
-                                ctypes.byref(comp_bytes), ctypes.byref(n_off)),
+    begin = lib.tans_encode_packed_begin if packed else lib.tans_encode_begin
+    check(begin(_ptr(symbols), K, S, _ptr(freqs), freqs.numel(), _ptr(spread),
+                L.bit_length() - 1, ctypes.byref(handle), ctypes.byref(comp_bytes),
+                ctypes.byref(n_off)),
           "tans_encode_interleaved")
     try:
         comp = torch.empty(comp_bytes.value, dtype=torch.uint8)
-        states = torch.empty(K, dtype=torch.uint16)
+        states = torch.empty(0 if packed else K, dtype=torch.uint16)
         offsets = torch.empty(n_off.value, dtype=torch.int64)
     except BaseException:
         lib.tans_encode_free(handle)
@@ -116,6 +120,23 @@ def _groups(K: int) -> int:
 
 def _sm_bytes(K: int, N: int) -> int:
     return ((N + TANS_TILE - 1) // TANS_TILE) * K * 8
+
+
+def _lanes(states: torch.Tensor, sm: torch.Tensor, N: int) -> int:
+    """K, the lanes of an encoding: states.numel(), or for the packed
+    layout (no state array) the sign/mantissa size over 8 bytes per tile."""
+    if states.numel() or N <= 0:
+        return states.numel()
+    per_lane = ((N + TANS_TILE - 1) // TANS_TILE) * 8
+    _require(sm.numel() % per_lane == 0, "sign/mantissa tensor has the wrong tiled size")
+    return sm.numel() // per_lane
+
+
+def _check_packed(packed: bool, N: int, log2L: int, K: int) -> None:
+    if packed and K:
+        _require(log2L == TANS_PAIR_LOG2L and N <= TANS_PACKED_MAX_N,
+                 f"an encoding without states (the packed layout) needs the pair table "
+                 f"and at most {TANS_PACKED_MAX_N} elements per stream")
 
 
 # (spread, freqs) pairs whose device table build reported no inconsistency:
@@ -167,10 +188,11 @@ def gpu_tans_decode(compressed: torch.Tensor, offsets: torch.Tensor, states: tor
     _check_dev("freqs", freqs, torch.int32)
     N = int(n_fp8_per_stream)
     _require(N >= 0 and N % 2 == 0, "n_fp8_per_stream must be even")
-    K = states.numel()
+    K = _lanes(states, sign_mantissa, N)
     _require(offsets.numel() == _groups(K) + 1, "offsets must have n_groups + 1 entries")
     _require(sign_mantissa.numel() == _sm_bytes(K, N), "sign_mantissa has the wrong shape")
     log2L = log2_states(spread.numel())
+    _check_packed(states.numel() == 0, N, log2L, K)
     nsym = freqs.numel()
     _require((nsym, log2L) in ((256, TANS_PAIR_LOG2L), (16, TANS_NIBBLE_LOG2L)),
              "freqs must hold 256 pair or 16 nibble frequencies matching the spread size")
@@ -278,14 +300,17 @@ def fp8_vecadd_fused_tans(a_comp: torch.Tensor, a_offsets: torch.Tensor, a_state
     _check_dev("decode_tbl", decode_tbl, torch.int32)
     N = int(n_fp8_per_stream)
     _require(N >= 0 and N % 16 == 0, "n_fp8_per_stream must be divisible by 16")
-    K = a_states.numel()
-    _require(b_states.numel() == K, "A/B stream counts must match")
+    K = _lanes(a_states, a_sm, N)
+    _require((a_states.numel() == 0) == (b_states.numel() == 0),
+             "A and B must share a layout (both with states, or both packed)")
+    _require(_lanes(b_states, b_sm, N) == K, "A/B stream counts must match")
     _require(a_offsets.numel() == _groups(K) + 1 and b_offsets.numel() == _groups(K) + 1,
              "offset tensors must have n_groups + 1 entries")
     _require(a_sm.numel() == _sm_bytes(K, N) and b_sm.numel() == _sm_bytes(K, N),
              "sign/mantissa tensors have the wrong tiled size")
     _require(decode_tbl.numel() % 2 == 0, "decode_tbl must hold 2 words per state")
     log2L = log2_states(decode_tbl.numel() // 2)
+    _check_packed(a_states.numel() == 0, N, log2L, K)
     dev = a_comp.device
     for t in (a_offsets, a_states, a_sm, b_comp, b_offsets, b_states, b_sm, decode_tbl):
         _require(t.device == dev, "all tensors must be on one device")

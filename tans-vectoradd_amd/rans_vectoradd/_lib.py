@@ -19,6 +19,7 @@ EXPORTS = (
     "tans_encode_begin",
     "tans_encode_finish",
     "tans_encode_free",
+    "tans_encode_packed_begin",
     "tans_fp8_memcpy",
     "tans_fp8_vecadd_raw",
     "tans_stream_probe",
@@ -40,6 +41,7 @@ TANS_GEMM_MAX_BATCH = 8
 TANS_GEMM_MAX_SEG_COLS = 1024
 TANS_PAIR_LOG2L = 12
 TANS_NIBBLE_LOG2L = 11
+TANS_PACKED_MAX_N = 64     # the packed layout's longest lane (pair alphabet)
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(
@@ -59,6 +61,8 @@ for _name, _args in {
     "tans_build_decode_table": [_P, _P, _I32, _I32, _P],
     "tans_encode_begin": [_P, _I64, _I64, _P, _I32, _P, _I32, ctypes.POINTER(_P),
                           ctypes.POINTER(_I64), ctypes.POINTER(_I64)],
+    "tans_encode_packed_begin": [_P, _I64, _I64, _P, _I32, _P, _I32, ctypes.POINTER(_P),
+                                 ctypes.POINTER(_I64), ctypes.POINTER(_I64)],
     "tans_encode_finish": [_P, _P, _P, _P],
     "tans_fp8_memcpy": [_P, _P, _I64, _P],
     "tans_fp8_vecadd_raw": [_P, _P, _P, _I64, _P],

@@ -13,16 +13,18 @@ the metadata key ``tans:name`` with a JSON description:
   for a TansMatrix (the layout of fp8_gemm_fused_tans).
 
 Plain tensors (scales, unencoded weights) are stored under their own names;
-``tans_format`` in the metadata names the layout version: v4 streams follow
+``tans_format`` in the metadata names the layout version: v5 streams follow
 the carry-driven refill schedule (segments of two steps for the pair
 alphabet; 3, 3 and 2 steps for the nibble alphabet, whose tables give every
 present symbol a frequency of at least 2) with a plain check before a last
-16-element tile of one segment, and matrices the 16-row matrix-core lane
-groups (include/tans_amd.h).  v3 files are read unless an entry of lanes has
-such a last tile (N > 16 and N % 16 in 1..4 with pairs, 1..3 with nibbles:
-there v3 applied the final check), v2 files under the same condition when
-all their entries use the pair alphabet; files of other versions are
-refused.
+16-element tile of one segment, or, for entries of lanes whose ``states``
+part is empty, the packed layout of short streams (pair alphabet, N <= 64);
+matrices use the 16-row matrix-core lane groups (include/tans_amd.h).  v4
+files are v5 files without packed entries.  v3 files are read unless an
+entry of lanes has such a last tile (N > 16 and N % 16 in 1..4 with pairs,
+1..3 with nibbles: there v3 applied the final check), v2 files under the
+same condition when all their entries use the pair alphabet; files of other
+versions are refused.
 """
 from __future__ import annotations
 
@@ -32,7 +34,8 @@ import torch
 
 from .tans_codec import TansMatrix, TansTensor
 
-FORMAT = "tans-wave64-v4"
+FORMAT = "tans-wave64-v5"
+_NO_PACKED = "tans-wave64-v4"   # v5 without packed entries
 _PREV = "tans-wave64-v3"        # differs only where _last_tile_rule_changed
 _PAIR_ONLY = "tans-wave64-v2"   # pair entries: as v3
 
@@ -92,7 +95,7 @@ def load(path: str, device="cpu") -> dict:
     with safe_open(path, framework="pt", device="cpu") as f:
         meta = f.metadata() or {}
         fmt = meta.get("tans_format")
-        if fmt not in (FORMAT, _PREV, _PAIR_ONLY):
+        if fmt not in (FORMAT, _NO_PACKED, _PREV, _PAIR_ONLY):
             raise ValueError(f"{path}: not a {FORMAT} container (format {fmt!r}); "
                              "re-encode it with this version")
         keys = set(f.keys())
@@ -102,7 +105,7 @@ def load(path: str, device="cpu") -> dict:
                              "streams follow the previous refill schedule; re-encode it with "
                              "this version")
         changed = [n for n, d in encoded.items() if _last_tile_rule_changed(d)]
-        if fmt != FORMAT and changed:
+        if fmt in (_PREV, _PAIR_ONLY) and changed:
             raise ValueError(f"{path}: {fmt} container whose entries {changed} end in a tile of "
                              "one refill segment, where that version's last check differs; "
                              "re-encode them with this version")

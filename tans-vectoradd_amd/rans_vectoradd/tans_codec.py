@@ -21,8 +21,8 @@ import numpy as np
 import torch
 
 from . import _C
-from ._lib import (TANS_GEMM_MAX_SEG_COLS, TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PAIR_LOG2L,
-                   check, lib)
+from ._lib import (TANS_GEMM_MAX_SEG_COLS, TANS_LANES, TANS_NIBBLE_LOG2L, TANS_PACKED_MAX_N,
+                   TANS_PAIR_LOG2L, check, lib)
 
 PAIR_L = 1 << TANS_PAIR_LOG2L
 NIBBLE_L = 1 << TANS_NIBBLE_LOG2L
@@ -168,7 +168,25 @@ def _check_tile(tile: int, N: int) -> None:
         raise ValueError(f"tile must be 0 or divide N / 2 = {N // 2}; got {tile}")
 
 
-def encode(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair"):
+LAYOUTS = ("auto", "words", "packed")
+
+
+def packed_layout(N: int, alphabet: str, layout: str = "auto") -> bool:
+    """Whether encode() writes the packed layout of short streams for lanes
+    of N elements: "packed" asks for it (pair alphabet, 2 <= N <= 64),
+    "words" for the refill-schedule layout, and "auto" takes the packed
+    one wherever it applies."""
+    if layout not in LAYOUTS:
+        raise ValueError(f"layout must be one of {LAYOUTS}")
+    fits = alphabet == "pair" and 2 <= N <= TANS_PACKED_MAX_N
+    if layout == "packed" and not fits:
+        raise ValueError(f"the packed layout needs the pair alphabet and 2 <= N <= "
+                         f"{TANS_PACKED_MAX_N}")
+    return fits and layout != "words"
+
+
+def encode(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair",
+           layout: str = "auto"):
     """tANS-encode FP8 bytes [K, N] (K lanes of N elements, N even).
 
     Returns the reference's 7-tuple: (compressed uint8, states uint16 [K],
@@ -176,7 +194,11 @@ def encode(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str =
     freqs int32, spread int32).  ``tile`` is accepted as the reference
     accepts it (rans_vectoradd/tans_codec.py:115-120: 0, or any tile that
     divides N / 2; otherwise it raises), but the sign/mantissa layout here
-    is always the 16-element tiles that both decoders read."""
+    is always the 16-element tiles that both decoders read.  ``layout``
+    (packed_layout): lanes of at most 64 elements with the pair alphabet
+    are written in the packed layout by default, whose states live in the
+    streams (``states`` is then empty); the decoders tell the layouts apart
+    by that."""
     if not (isinstance(fp8_bytes, torch.Tensor) and fp8_bytes.dim() == 2
             and fp8_bytes.dtype == torch.uint8):
         raise ValueError("fp8_bytes must be a 2-D uint8 tensor [K, N]")
@@ -186,6 +208,7 @@ def encode(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str =
     if N % 2:
         raise ValueError("N must be even")
     _check_tile(tile, N)
+    packed = packed_layout(N, alphabet, layout)
     if isinstance(exp_freqs, torch.Tensor):
         exp_freqs = exp_freqs.detach().cpu().float().numpy()
     freqs = symbol_freqs(exp_freqs, alphabet)
@@ -193,7 +216,8 @@ def encode(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str =
     symbols, sm = split_fp8(fp8_bytes.cpu(), alphabet)
     freqs_t = torch.from_numpy(freqs)
     spread_t = torch.from_numpy(spread)
-    comp, states, offsets, partial = _C.tans_encode_interleaved(symbols, freqs_t, spread_t)
+    comp, states, offsets, partial = _C.tans_encode_interleaved(symbols, freqs_t, spread_t,
+                                                                packed=packed)
     return comp, states, offsets, partial, sm, freqs_t, spread_t
 
 
@@ -319,14 +343,18 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
         wp[:R, :C] = w
         w = wp
     slab = gemm_slab(w, S, Nc)
-    enc = encode_gpu if slab.is_cuda else encode
-    comp, states, offsets, partial, sm, freqs, spread = enc(slab, exp_freqs, alphabet=alphabet)
+    # the GEMM kernel reads the refill-schedule layout (encode_gpu's only one)
+    if slab.is_cuda:
+        enc = encode_gpu(slab, exp_freqs, alphabet=alphabet)
+    else:
+        enc = encode(slab, exp_freqs, alphabet=alphabet, layout="words")
+    comp, states, offsets, partial, sm, freqs, spread = enc
     return TansMatrix(comp, states, offsets, partial, sm, freqs, spread, rows=R, cols=C,
                       segments=S, seg_cols=Nc, alphabet=alphabet)
 
 
 # ---------------------------------------------------------------------------
-# GPU encoder (the same bytes as encode(), from FP8 bytes on the device)
+# GPU encoder (the bytes of encode(..., layout="words"), from FP8 bytes on the device)
 # ---------------------------------------------------------------------------
 
 _ENC_TABLES: dict = {}
@@ -367,8 +395,10 @@ def _encode_tables(exp_freqs, alphabet: str, dev: torch.device):
 
 def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair"):
     """encode() on the GPU: FP8 bytes [K, N] (uint8, on a GPU, N even) ->
-    the same 7-tuple with the same bytes, as device tensors (freqs and
-    spread included, ready for gpu_tans_decode).  Reads the stream length
+    the 7-tuple of encode(..., layout="words") with the same bytes, as
+    device tensors (freqs and spread included, ready for gpu_tans_decode).
+    It writes the refill-schedule layout only, which every decoder reads at
+    any N.  Reads the stream length
     back from the device once (the size of the compressed tensor)."""
     if not (isinstance(fp8_bytes, torch.Tensor) and fp8_bytes.dim() == 2
             and fp8_bytes.dtype == torch.uint8):

@@ -24,14 +24,19 @@ def T():
     return tans_codec
 
 
-def _encode_check(T, fp8, exp_freqs, alphabet):
+# (alphabet, layout): the refill-schedule layout of both alphabets and, for
+# lanes of at most 64 elements, the packed layout ("auto" picks it there)
+CODECS = [("pair", "words"), ("pair", "auto"), ("nibble", "auto")]
+
+
+def _encode_check(T, fp8, exp_freqs, alphabet, layout="auto"):
     K, N = fp8.shape
     log2L, sps = ALPHABETS[alphabet]
-    comp, st, off, part, sm, fr, sp = T.encode(fp8, exp_freqs, alphabet=alphabet)
-    dec = O.w64_decode(comp.numpy(), off.numpy(), st.numpy(), sm.numpy(), sp.numpy(), fr.numpy(),
-                       log2L, sps, K, N)
+    enc = T.encode(fp8, exp_freqs, alphabet=alphabet, layout=layout)
+    assert (enc[1].numel() == 0) == (K > 0 and T.packed_layout(N, alphabet, layout))
+    dec = O.layout_decode(enc, K, N, log2L, sps)
     assert np.array_equal(dec, fp8.numpy())
-    return comp, st, off, part, sm, fr, sp
+    return enc
 
 
 def test_quantize_freqs_matches_reference_golden(T):
@@ -136,17 +141,19 @@ def test_decode_table_matches_oracle_slot_table(T, alphabet):
         assert np.array_equal((tbl[:, 0] >> 19) & 0xF, sym & 0xF)
 
 
-@pytest.mark.parametrize("alphabet", list(ALPHABETS))
+@pytest.mark.parametrize("alphabet,layout", CODECS)
 @pytest.mark.parametrize("K,N", [(128, 128), (1024, 128), (10000, 128), (64, 2), (65, 18),
-                                 (200, 130), (3, 1000), (1, 16), (127, 4096)])
-def test_encode_roundtrip_reference_test_cases(T, alphabet, K, N):
+                                 (200, 130), (3, 1000), (1, 16), (127, 4096), (130, 64),
+                                 (63, 46)])
+def test_encode_roundtrip_reference_test_cases(T, alphabet, layout, K, N):
     """Cases of the reference's test_gpu_decode_tans.py:69-74 (seed 42, Qwen3
     histogram) plus ragged shapes: K not a multiple of 64, N not a multiple of
     16, a single lane, N = 2."""
     from rans_vectoradd import data as D
     torch.manual_seed(42)
     fp8 = D.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
-    comp, st, off, part, sm, fr, sp = _encode_check(T, fp8, torch.tensor(D.QWEN3_14B_FP8_EXP), alphabet)
+    comp, st, off, part, sm, fr, sp = _encode_check(T, fp8, torch.tensor(D.QWEN3_14B_FP8_EXP),
+                                                    alphabet, layout)
     off = off.numpy()
     assert off[0] == 0 and (np.diff(off) >= 0).all() and (off % 4 == 0).all()
     words = comp.numpy().view(np.uint32)
@@ -170,7 +177,7 @@ def test_encode_roundtrip_last_tile_of_one_segment(T, alphabet, N):
     K = 2000
     g = torch.Generator().manual_seed(N)
     fp8 = torch.randint(0, 256, (K, N), dtype=torch.uint8, generator=g)
-    _encode_check(T, fp8, torch.tensor(D.QWEN3_14B_FP8_EXP), alphabet)
+    _encode_check(T, fp8, torch.tensor(D.QWEN3_14B_FP8_EXP), alphabet, "words")
 
 
 def test_config0_cpu_roundtrip_bits_per_byte(T):
@@ -298,6 +305,7 @@ def test_encode_matrix_slab_layout(T, alphabet, R, C, S):
         assert m.segments <= S
     log2L, sps = ALPHABETS[alphabet]
     K = m.segments * Rp * 4
+    assert m.states.numel() == K       # the GEMM reads the refill-schedule layout
     dec = O.w64_decode(m.comp.numpy(), m.offsets.numpy(), m.states.numpy(), m.sm.numpy(),
                        m.spread.numpy(), m.freqs.numpy(), log2L, sps, K, Nc // 4)
     pad = int(np.argmax(hist.numpy())) << 3

@@ -16,8 +16,7 @@ LOG2L = {"pair": (12, 2), "nibble": (11, 1)}
 
 def _decode_lanes(e):
     log2L, sps = LOG2L[e.alphabet]
-    return O.w64_decode(e.comp.numpy(), e.offsets.numpy(), e.states.numpy(), e.sm.numpy(),
-                        e.spread.numpy(), e.freqs.numpy(), log2L, sps, e.K, e.N)
+    return O.layout_decode(e.as_tuple(), e.K, e.N, log2L, sps)
 
 
 def _decode_matrix(m):
@@ -93,7 +92,8 @@ def test_container_reads_v2_pair_entries_only(tmp_path):
     q, _ = D.gaussian_fp8_bytes(64 * 32, seed=3)
     for alphabet, ok in (("pair", True), ("nibble", False)):
         t = T.TansTensor.from_tuple(T.encode(q.reshape(64, 32), D.exp_histogram(q),
-                                             alphabet=alphabet), 64, 32, alphabet)
+                                             alphabet=alphabet, layout="words"),
+                                    64, 32, alphabet)
         path = os.path.join(tmp_path, f"{alphabet}.safetensors")
         container.save(path, {"w": t})
         with safe_open(path, framework="pt") as f:
@@ -121,21 +121,39 @@ def test_container_reads_v3_unless_the_last_tile_rule_changed(tmp_path):
     for alphabet, N, ok in cases:
         q, _ = D.gaussian_fp8_bytes(64 * N, seed=N)
         t = T.TansTensor.from_tuple(T.encode(q.reshape(64, N), D.exp_histogram(q),
-                                             alphabet=alphabet), 64, N, alphabet)
+                                             alphabet=alphabet, layout="words"),
+                                    64, N, alphabet)
         path = os.path.join(tmp_path, f"{alphabet}{N}.safetensors")
         container.save(path, {"w": t})
         with safe_open(path, framework="pt") as f:
             meta, tensors = f.metadata(), {k: f.get_tensor(k) for k in f.keys()}
-        assert meta["tans_format"] == "tans-wave64-v4"
-        for old in ("tans-wave64-v3", "tans-wave64-v2") if alphabet == "pair" else ("tans-wave64-v3",):
+        assert meta["tans_format"] == "tans-wave64-v5"
+        olds = ("tans-wave64-v4", "tans-wave64-v3", "tans-wave64-v2")
+        for old in olds if alphabet == "pair" else olds[:2]:
             meta["tans_format"] = old
             prev = os.path.join(tmp_path, f"{alphabet}{N}_{old[-2:]}.safetensors")
             save_file(tensors, prev, metadata=meta)
-            if ok:
+            if ok or old.endswith("v4"):
                 assert torch.equal(container.load(prev)["w"].comp, t.comp)
             else:
                 with pytest.raises(ValueError, match="one refill segment"):
                     container.load(prev)
+
+
+@pytest.mark.parametrize("N", [16, 46, 64])
+def test_container_packed_entry_roundtrip(tmp_path, N):
+    """Entries of short lanes in the packed layout (no states: the part is
+    stored empty) load back unchanged and decode to the input."""
+    from rans_vectoradd import container, data as D, tans_codec as T
+    q, _ = D.gaussian_fp8_bytes(130 * N, seed=N)
+    t = T.TansTensor.from_tuple(T.encode(q.reshape(130, N), D.exp_histogram(q)), 130, N, "pair")
+    assert t.states.numel() == 0
+    path = os.path.join(tmp_path, "p.safetensors")
+    container.save(path, {"p": t})
+    got = container.load(path)["p"]
+    for part in ("comp", "states", "offsets", "sm", "freqs", "spread"):
+        assert torch.equal(getattr(got, part), getattr(t, part)), part
+    assert np.array_equal(_decode_lanes(got), q.reshape(130, N).numpy())
 
 
 def _checkpoint(path):

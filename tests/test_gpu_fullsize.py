@@ -4,7 +4,8 @@ do not depend on size:
 * config 1 (2^29 elements per vector): the fused tANS add equals the raw add
   on every element, and the raw add equals the oracle's add table (RNE,
   satfinite) on every element, so the fused output is pinned to the oracle;
-  the headline encoding stays within 7 bits per FP8 byte;
+  the headline encoding stays within 7 bits per FP8 byte, and the packed
+  layout's 1Ki / 4Ki streams within 7.8 / 7.0;
 * config 2 (2^30 elements): the standalone decode returns its input, for
   both tables (Gaussian and Laplace data) and both alphabets;
 * the GPU encoder's bytes at 2^29 elements equal the CPU encoder's.
@@ -73,6 +74,30 @@ def test_vecadd_config1_full_size(R, vectors, alphabet, lane):
     if alphabet == "pair" and lane == 1024:
         bits = 8 * (T.compressed_bytes(*ea[:5]) + T.compressed_bytes(*eb[:5])) / (2 * VEC_ELEMS)
         assert bits <= 7.0, f"{bits:.3f} bits per FP8 byte"
+
+
+@pytest.mark.parametrize("lane,max_bits", [(16, 7.8), (64, 7.0)])
+def test_vecadd_config1_full_size_packed(R, vectors, lane, max_bits):
+    """1Ki- and 4Ki-element streams (16 and 64 per lane) in the packed
+    layout, encoded on the CPU: fused == raw on all 2^29 elements, at most
+    7.8 and 7.0 bits per FP8 byte."""
+    from rans_vectoradd import tans_codec as T
+    qa, qb, hist, raw = vectors
+    _say(f"case: fused vecadd 2^29 pair {lane} per lane, packed layout")
+    K = VEC_ELEMS // lane
+    ea = T.encode(qa.cpu().reshape(K, lane), hist.numpy())
+    eb = T.encode(qb.cpu().reshape(K, lane), hist.numpy())
+    assert ea[1].numel() == 0 and eb[1].numel() == 0
+    bits = 8 * (T.compressed_bytes(*ea[:5]) + T.compressed_bytes(*eb[:5])) / (2 * VEC_ELEMS)
+    assert bits <= max_bits, f"{bits:.3f} bits per FP8 byte"
+    tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy()).cuda()
+    order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
+    a = [ea[i].cuda() for i in order]
+    b = [eb[i].cuda() for i in order]
+    del ea, eb
+    out = R.fp8_vecadd_fused_tans(*a, *b, tbl, lane)
+    fused = out.view(lane // 16, K, 16).permute(1, 0, 2).reshape(-1)
+    assert torch.equal(fused, raw)
 
 
 @pytest.mark.parametrize("alphabet", ["pair", "nibble"])

@@ -14,6 +14,15 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 ALPHABETS = ["pair", "nibble"]
+# alphabet[:layout] for the tests with lanes of at most 64 elements, where
+# "pair" means the packed layout and "pair:words" the refill-schedule one
+CODECS = ["pair", "pair:words", "nibble"]
+
+
+def _codec(codec):
+    """encode() keywords of a CODECS entry."""
+    alphabet, _, layout = codec.partition(":")
+    return dict(alphabet=alphabet, layout=layout or "auto")
 
 
 def _say(msg):
@@ -122,7 +131,7 @@ def test_table_device_any_spread(R, alphabet):
     assert status.item() == 0
 
 
-@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("alphabet", CODECS)
 @pytest.mark.parametrize("K,N", [(128, 128), (1024, 128), (10000, 128), (100000, 128),
                                  (64, 2), (65, 18), (200, 130), (3, 1000),
                                  (130, 30), (192, 64), (66, 80), (1, 16), (4096, 14),
@@ -139,7 +148,7 @@ def test_decode_roundtrip(R, alphabet, K, N):
     exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
     torch.manual_seed(42)
     fp8 = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
-    comp, st, off, part, sm, fr, sp = T.encode(fp8, exp_freqs, alphabet=alphabet)
+    comp, st, off, part, sm, fr, sp = T.encode(fp8, exp_freqs, **_codec(alphabet))
     dec = R.gpu_tans_decode(comp.cuda(), off.cuda(), st.cuda(), part.cuda(), sm.cuda(),
                             sp.cuda(), fr.cuda(), N)
     got = dec.cpu().t().contiguous()
@@ -164,7 +173,8 @@ def test_decode_last_tile_of_one_segment(R, alphabet, N, K):
     fp8 = torch.randint(0, 256, (K, N), dtype=torch.uint8, generator=g)
     exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
     comp, st, off, part, sm, fr, sp = [x.cuda() for x in T.encode(fp8, exp_freqs,
-                                                                  alphabet=alphabet)]
+                                                                  alphabet=alphabet,
+                                                                  layout="words")]
     dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
     got = dec.cpu().t().contiguous()
     assert torch.equal(got, fp8), f"{(got != fp8).sum().item()} mismatched bytes"
@@ -240,7 +250,7 @@ def test_table_device_rejects_what_the_host_rejects(R, alphabet):
         R.gpu_tans_decode(comp, off, st, part, sm, sp, fr_bad, N)
 
 
-@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("alphabet", CODECS)
 @pytest.mark.parametrize("K,N", [(1024, 128), (10000, 256), (1024, 1024), (64, 16), (70, 32),
                                  (4160, 64), (130, 80), (1, 16), (5, 64), (127, 32)])
 def test_vecadd_fused_vs_raw_and_oracle(R, lut, alphabet, K, N):
@@ -254,8 +264,8 @@ def test_vecadd_fused_vs_raw_and_oracle(R, lut, alphabet, K, N):
     torch.manual_seed(0)
     fa = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
     fb = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
-    ca, sa, oa, pa, sma, pf, sp = T.encode(fa, exp_freqs, tile=8, alphabet=alphabet)
-    cb, sb, ob, pb, smb, _, _ = T.encode(fb, exp_freqs, tile=8, alphabet=alphabet)
+    ca, sa, oa, pa, sma, pf, sp = T.encode(fa, exp_freqs, tile=8, **_codec(alphabet))
+    cb, sb, ob, pb, smb, _, _ = T.encode(fb, exp_freqs, tile=8, **_codec(alphabet))
     tbl = T.build_decode_table(sp.numpy(), pf.numpy())
     args = [t.cuda() for t in (ca, oa, sa, pa, sma, cb, ob, sb, pb, smb, tbl)]
     raw = R.fp8_vecadd_raw(fa.flatten().cuda(), fb.flatten().cuda()).cpu().reshape(K, N)
@@ -266,7 +276,7 @@ def test_vecadd_fused_vs_raw_and_oracle(R, lut, alphabet, K, N):
     assert ok.all()
 
 
-@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("alphabet", CODECS)
 @pytest.mark.parametrize("K,N", [(600001, 18), (1048617, 16)])
 def test_decode_several_group_pairs_per_wave(R, alphabet, K, N):
     """Columns of one or two tiles run one workgroup per CU (8192 group
@@ -279,14 +289,14 @@ def test_decode_several_group_pairs_per_wave(R, alphabet, K, N):
     exp_freqs = torch.tensor(R.QWEN3_14B_FP8_EXP, dtype=torch.float64)
     torch.manual_seed(K)
     fp8 = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
-    comp, st, off, part, sm, fr, sp = T.encode(fp8, exp_freqs, alphabet=alphabet)
+    comp, st, off, part, sm, fr, sp = T.encode(fp8, exp_freqs, **_codec(alphabet))
     dec = R.gpu_tans_decode(comp.cuda(), off.cuda(), st.cuda(), part.cuda(), sm.cuda(),
                             sp.cuda(), fr.cuda(), N)
     got = dec.cpu().t().contiguous()
     assert torch.equal(got, fp8), f"{(got != fp8).sum().item()} mismatched bytes"
 
 
-@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("alphabet", CODECS)
 @pytest.mark.parametrize("K,N", [(300037, 16), (270000, 48)])
 def test_vecadd_fused_several_groups_per_wave(R, lut, alphabet, K, N):
     """The fused kernel runs at most one workgroup per CU (4096 waves on
@@ -301,8 +311,8 @@ def test_vecadd_fused_several_groups_per_wave(R, lut, alphabet, K, N):
     torch.manual_seed(K + N)
     fa = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
     fb = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
-    ca, sa, oa, pa, sma, pf, sp = T.encode(fa, exp_freqs, alphabet=alphabet)
-    cb, sb, ob, pb, smb, _, _ = T.encode(fb, exp_freqs, alphabet=alphabet)
+    ca, sa, oa, pa, sma, pf, sp = T.encode(fa, exp_freqs, **_codec(alphabet))
+    cb, sb, ob, pb, smb, _, _ = T.encode(fb, exp_freqs, **_codec(alphabet))
     tbl = T.build_decode_table(sp.numpy(), pf.numpy())
     args = [t.cuda() for t in (ca, oa, sa, pa, sma, cb, ob, sb, pb, smb, tbl)]
     fused = T.untile(R.fp8_vecadd_fused_tans(*args, N).cpu(), K, N)
@@ -351,7 +361,7 @@ def test_vecadd_gaussian_2p24(R, lut, alphabet):
     assert np.array_equal(fused, ref)
 
 
-@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("alphabet", CODECS)
 @pytest.mark.parametrize("N", [64, 256])
 def test_vecadd_gaussian_short_streams(R, lut, alphabet, N):
     """Config-1 sweep points below the headline: 64 and 256 elements per
@@ -364,8 +374,8 @@ def test_vecadd_gaussian_short_streams(R, lut, alphabet, N):
     qa, _ = D.gaussian_fp8_bytes(n, seed=11)
     qb, _ = D.gaussian_fp8_bytes(n, seed=12)
     hist = D.exp_histogram(torch.cat([qa, qb]))
-    ea = T.encode(qa.reshape(K, N), hist, tile=8, alphabet=alphabet)
-    eb = T.encode(qb.reshape(K, N), hist, tile=8, alphabet=alphabet)
+    ea = T.encode(qa.reshape(K, N), hist, tile=8, **_codec(alphabet))
+    eb = T.encode(qb.reshape(K, N), hist, tile=8, **_codec(alphabet))
     tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy())
     order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
     args = [x.cuda() for x in (*[ea[i] for i in order], *[eb[i] for i in order], tbl)]
@@ -385,7 +395,7 @@ def _few_exponent_bytes(K, N, exps, seed):
     return (((sm >> 3) << 7) | (e << 3) | m).to(torch.uint8)
 
 
-@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("alphabet", CODECS)
 @pytest.mark.parametrize("exps_a,exps_b", [((7,), (7,)), ((15,), (15,)), ((0,), (9,)),
                                            ((7, 8), (7, 8)), ((3,), (3, 12))])
 def test_few_exponents_zero_bit_steps(R, lut, alphabet, exps_a, exps_b):
@@ -401,8 +411,8 @@ def test_few_exponents_zero_bit_steps(R, lut, alphabet, exps_a, exps_b):
     fa = _few_exponent_bytes(K, N, exps_a, seed=1)
     fb = _few_exponent_bytes(K, N, exps_b, seed=2)
     hist = np.bincount(((torch.cat([fa, fb]).numpy() >> 3) & 15).ravel(), minlength=16)
-    ea = T.encode(fa, hist, tile=8, alphabet=alphabet)
-    eb = T.encode(fb, hist, tile=8, alphabet=alphabet)
+    ea = T.encode(fa, hist, tile=8, **_codec(alphabet))
+    eb = T.encode(fb, hist, tile=8, **_codec(alphabet))
     if len(set(exps_a) | set(exps_b)) == 1:
         tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy()).view(-1, 2)
         assert ((tbl[:, 0] & 0x1F) == 0).all()          # every entry reads 0 bits
@@ -410,9 +420,11 @@ def test_few_exponents_zero_bit_steps(R, lut, alphabet, exps_a, exps_b):
         comp, st, off, part, sm, fr, sp = [x.cuda() for x in e]
         dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
         assert torch.equal(dec.cpu().t().contiguous(), f)
-        g = T.encode_gpu(f.cuda(), hist, tile=8, alphabet=alphabet)
+        # the GPU encoder writes the refill-schedule layout
+        g = T.encode_gpu(f.cuda(), hist, tile=8, alphabet=_codec(alphabet)["alphabet"])
+        w = T.encode(f, hist, tile=8, alphabet=_codec(alphabet)["alphabet"], layout="words")
         for i in (0, 1, 2, 4, 5, 6):
-            assert torch.equal(g[i].cpu(), e[i]), f"GPU encoder output {i} differs"
+            assert torch.equal(g[i].cpu(), w[i]), f"GPU encoder output {i} differs"
     tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy())
     order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
     args = [x.cuda() for x in (*[ea[i] for i in order], *[eb[i] for i in order], tbl)]
@@ -452,7 +464,7 @@ def test_streams_consumed_near_the_feed_limit(R, lut, alphabet):
     assert ok.all()
 
 
-@pytest.mark.parametrize("alphabet", ALPHABETS)
+@pytest.mark.parametrize("alphabet", CODECS)
 @pytest.mark.parametrize("N", [16, 32, 48, 64, 80])
 def test_longest_short_streams(R, lut, alphabet, N):
     """Streams at the most words a lane can take: every exponent 15, coded
@@ -469,8 +481,8 @@ def test_longest_short_streams(R, lut, alphabet, N):
     sm = torch.where((sm & 7) == 7, sm - 1, sm)          # mantissa 7 with exponent 15 is NaN
     fa, fb = ((sm & 8) << 4) | (15 << 3) | (sm & 7)
     steep = torch.tensor([2.0 ** -e for e in range(16)], dtype=torch.float64)
-    ea = T.encode(fa, steep, tile=8, alphabet=alphabet)
-    eb = T.encode(fb, steep, tile=8, alphabet=alphabet)
+    ea = T.encode(fa, steep, tile=8, **_codec(alphabet))
+    eb = T.encode(fb, steep, tile=8, **_codec(alphabet))
     comp, st, off, part, smp, fr, sp = [x.cuda() for x in ea]
     dec = R.gpu_tans_decode(comp, off, st, part, smp, sp, fr, N)
     assert torch.equal(dec.cpu().t().contiguous(), fa)

@@ -21,7 +21,8 @@ def _cases(n, seed):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(n):
-        alphabet = ("pair", "nibble")[i % 2]
+        # "pair" takes the packed layout up to 4 tiles, "pair:words" the other
+        alphabet = ("pair", "nibble", "pair:words")[i % 3]
         K = int(rng.choice([1, 13, 64, 65, 127, 200, 640, 1000, 4095]))
         tiles = int(rng.choice([1, 2, 3, 4, 5, 9]))
         table = ("data", "qwen", "steep")[int(rng.integers(3))]
@@ -38,6 +39,12 @@ def _bytes(K, N, table, seed, R):
     fp8 = torch.randint(0, 256, (K, N), dtype=torch.uint8, generator=g)
     probs = R.QWEN3_14B_FP8_EXP if table == "qwen" else STEEP
     return fp8, torch.tensor(probs, dtype=torch.float64)
+
+
+def _codec(codec):
+    """encode() keywords of an alphabet[:layout] case."""
+    alphabet, _, layout = codec.partition(":")
+    return dict(alphabet=alphabet, layout=layout or "auto")
 
 
 @pytest.fixture(scope="module")
@@ -58,8 +65,8 @@ def test_fused_random_shape(R, lut, alphabet, K, tiles, table, seed):
     if table == "data":
         hist = np.bincount(((torch.cat([fa, fb]).numpy() >> 3) & 15).ravel(), minlength=16)
         probs = torch.tensor(hist / hist.sum(), dtype=torch.float64)
-    ea = T.encode(fa, probs, tile=8, alphabet=alphabet)
-    eb = T.encode(fb, probs, tile=8, alphabet=alphabet)
+    ea = T.encode(fa, probs, tile=8, **_codec(alphabet))
+    eb = T.encode(fb, probs, tile=8, **_codec(alphabet))
     tbl = T.build_decode_table(ea[6].numpy(), ea[5].numpy())
     order = (0, 2, 1, 3, 4)   # comp, offsets, states, partial, sm
     args = [x.cuda() for x in (*[ea[i] for i in order], *[eb[i] for i in order], tbl)]
@@ -78,7 +85,7 @@ def test_decode_random_shape(R, alphabet, K, tiles, table, seed):
     print(f"case: decode K={K} N={N} {alphabet} table={table} seed={seed}", flush=True)
     torch.manual_seed(seed)
     fp8, probs = _bytes(K, N, table, seed, R)
-    enc = [x.cuda() for x in T.encode(fp8, probs, alphabet=alphabet)]
+    enc = [x.cuda() for x in T.encode(fp8, probs, **_codec(alphabet))]
     comp, st, off, part, sm, fr, sp = enc
     dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
     got = dec.cpu().t().contiguous()
