@@ -181,8 +181,9 @@ int tans_build_decode_table_device(const int32_t* spread, const int32_t* freqs,
 /* Fused decode of two encodings (same table) + FP8 add.
  * out is tiled [N/16, K, 16]: out[(t*K + k)*16 + i] = element 16t+i of
  * lane k.  N % 16 == 0.  comp_bytes_* bound the reads: malformed offsets
- * cannot make a kernel read outside the buffers.  Replaces
- * fp8_vecadd_fused_tans, csrc/vecadd.cu:290-393.                        */
+ * cannot make a kernel read outside the buffers.  a_states and b_states
+ * both NULL: both encodings are in the packed layout (log2L 12, N <= 64).
+ * Replaces fp8_vecadd_fused_tans, csrc/vecadd.cu:290-393.               */
 int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes,
                           const int64_t* a_offsets, const uint16_t* a_states,
                           const void* a_sm,
@@ -193,7 +194,8 @@ int tans_fp8_vecadd_fused(const void* a_comp, int64_t a_comp_bytes,
                           int64_t K, int64_t N, void* out, void* stream);
 
 /* Standalone decode to FP8 bytes, out [N, K] (element-major, lane-minor).
- * N even.  Replaces gpu_tans_decode, csrc/tans_decode.cu:159-210.       */
+ * N even.  states NULL: the packed layout (log2L 12, N <= 64).  Replaces
+ * gpu_tans_decode, csrc/tans_decode.cu:159-210.                         */
 int tans_decode(const void* comp, int64_t comp_bytes, const int64_t* offsets,
                 const uint16_t* states, const void* sm,
                 const uint32_t* table, int32_t log2L,
