@@ -168,24 +168,18 @@ def make_inputs(seed: int):
 
 
 def encode_pair(qa_d, qb_d, hist, lane: int, alphabet: str, layout: str = "auto"):
-    """Encode a and b with the GPU encoder (the same bytes as the CPU one),
-    or, where encode() picks the packed layout of short streams (pair
-    alphabet, at most 64 elements per lane), with the CPU encoder; returns
-    the device argument list of fp8_vecadd_fused_tans, the compressed byte
-    count and the encode time of both."""
+    """Encode a and b with the GPU encoder (the same bytes as the CPU one;
+    `layout` as in encode(): the packed layout of short streams where it
+    applies); returns the device argument list of fp8_vecadd_fused_tans, the
+    compressed byte count and the encode time of both."""
     import torch
     from rans_vectoradd import tans_codec as T
 
     K = N_ELEMS // lane
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    if T.packed_layout(lane, alphabet, layout):
-        h = hist.cpu().numpy()
-        ea = [x.cuda() for x in T.encode(qa_d.cpu().reshape(K, lane), h, alphabet=alphabet)]
-        eb = [x.cuda() for x in T.encode(qb_d.cpu().reshape(K, lane), h, alphabet=alphabet)]
-    else:
-        ea = T.encode_gpu(qa_d.reshape(K, lane), hist, tile=8, alphabet=alphabet)
-        eb = T.encode_gpu(qb_d.reshape(K, lane), hist, tile=8, alphabet=alphabet)
+    ea = T.encode_gpu(qa_d.reshape(K, lane), hist, tile=8, alphabet=alphabet, layout=layout)
+    eb = T.encode_gpu(qb_d.reshape(K, lane), hist, tile=8, alphabet=alphabet, layout=layout)
     torch.cuda.synchronize()
     t_enc = time.perf_counter() - t0
     tbl = T.build_decode_table(ea[6].cpu().numpy(), ea[5].cpu().numpy()).cuda()

@@ -224,6 +224,19 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
 int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* workspace,
                            const int64_t* offsets, void* comp, int64_t comp_bytes, void* stream);
 
+/* The GPU encoder into the packed layout of short streams (log2L 12, N <= 64):
+ * the same bytes as tans_encode_packed_begin/finish, with the same
+ * workspace, the same calls and no states output.  Replaces, like those,
+ * tans_encode_interleaved (csrc/tans_codec.cpp:69-196) for lanes of up to
+ * 64 FP8 bytes.                                                          */
+int tans_gpu_encode_packed_begin(const void* fp8, int64_t K, int64_t N, const uint32_t* enc_tab,
+                                 const uint16_t* enc_next, int32_t log2L, void* workspace,
+                                 int64_t workspace_bytes, int64_t* offsets, void* sm,
+                                 int32_t* status, void* stream);
+int tans_gpu_encode_packed_finish(int64_t K, int64_t N, int32_t log2L, const void* workspace,
+                                  const int64_t* offsets, void* comp, int64_t comp_bytes,
+                                  void* stream);
+
 /* ---------------- Fused decode + skinny GEMM (no counterpart in the
  * reference: its rows a15 / configs 3-4 are new) ----------------------- */
 

@@ -21,6 +21,12 @@
 //                        lane takes it, and the word is stored there when
 //                        its last bit is packed
 //   enc_sm_kernel        sign/mantissa tiles when rows are not whole tiles
+//
+// The packed layout of short streams (pair alphabet, at most 32 steps per
+// lane; schedule.h, tans_pack) reuses the backward pass, which then records
+// each lane's bit count and state in the workspace and sums the group's
+// bits into its stream size; enc_place_packed_kernel assembles each group's
+// stream (header of lane-pair counts, bit area) in LDS and copies it out.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -62,15 +68,19 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // Workspace layout: chunks u16 [S][K], glen u32 [G].
 struct WsLayout {
-    int64_t chunks, glen, total;
+    int64_t chunks, glen, plen, pstate, total;
 };
 
+// chunks [S][K] u16, glen [G] u32, and for the packed layout each lane's
+// bit count and initial state (u16 [K] each)
 WsLayout ws_layout(int64_t K, int64_t S) {
     const int64_t G = (K + kLanes - 1) / kLanes;
     WsLayout l;
     l.chunks = 0;
     l.glen = align256(S * K * 2);
-    l.total = l.glen + align256(G * 4);
+    l.plen = l.glen + align256(G * 4);
+    l.pstate = l.plen + align256(K * 2);
+    l.total = l.pstate + align256(K * 2);
     return l;
 }
 
@@ -210,13 +220,16 @@ __device__ __forceinline__ uint32_t lane_words(int64_t S, bool triple, uint32_t 
 // one go (the lanes' rows are N bytes apart, so a line read piecewise over
 // many steps could leave the cache in between).  A wave is one 64-lane
 // group (blocks hold four); its lanes' word counts are summed into
-// glen[group], padded to a multiple of 4.
-template <int SPS>
+// glen[group], padded to a multiple of 4.  PACKED (the packed layout):
+// plen[k] gets the lane's bits (12 for the state + its steps' nb), and
+// glen[group] the words of the group's stream (header, bits, padding to 16
+// bytes); `states` is then the workspace's state array.
+template <int SPS, bool PACKED = false>
 __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
     const uint8_t* __restrict__ fp8, int64_t K, int64_t N, const uint32_t* __restrict__ enc_tab,
     const uint16_t* __restrict__ next, int log2L, uint16_t* __restrict__ chunks,
     uint16_t* __restrict__ states, uint32_t* __restrict__ glen, uint32_t* __restrict__ sm,
-    int* __restrict__ status) {
+    int* __restrict__ status, uint16_t* __restrict__ plen) {
     static_assert(kEncBlock % kLanes == 0, "blocks hold whole groups");
     constexpr int NSYM = SPS == 2 ? 256 : 16;
     __shared__ uint2 tab[NSYM];
@@ -287,11 +300,21 @@ __global__ __launch_bounds__(kEncBlock) void enc_backward_kernel(
         }
         states[k] = (uint16_t)x;
         if (bad >> 31) *status = TANS_ESYMBOL;   // vector store: any failing lane may write it
-        words = lane_words(S, kTriple, bits, b1, b2);
+        if constexpr (PACKED) {
+            words = (uint32_t)tans_pack::kStateBits + bits;   // the lane's bits
+            plen[k] = (uint16_t)words;
+        } else {
+            words = lane_words(S, kTriple, bits, b1, b2);
+        }
     }
     #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) words += __shfl_xor(words, m, kLanes);
-    if ((threadIdx.x & (kLanes - 1)) == 0) glen[k / kLanes] = (words + 3u) & ~3u;
+    if ((threadIdx.x & (kLanes - 1)) == 0) {
+        if constexpr (PACKED)   // header + bits, padded to 16 bytes
+            glen[k / kLanes] = ((uint32_t)tans_pack::hdr_total(S) + (words + 7u) / 8u + 15u) / 16u * 4u;
+        else
+            glen[k / kLanes] = (words + 3u) & ~3u;
+    }
 }
 
 // offsets[g] = sum of glen[0..g), offsets[G] = total; one workgroup: each
@@ -443,6 +466,70 @@ __global__ __launch_bounds__(kEncBlock) void enc_place_kernel(
         __builtin_amdgcn_raw_buffer_store_b32(0u, out, (handed + (uint32_t)lane) * 4u, 0, 0);
 }
 
+// The packed layout: one wave per group.  Each lane reads its bit count
+// (plen), the pair's count is the two lanes' sum, and a scan of the counts
+// over the wave gives each pair's end; the wave then ORs the header and
+// every lane's bits (state minus L, then each step's chunk; even lanes
+// forwards from the pair's start, odd lanes bit-reversed backwards from its
+// end) into its LDS buffer, which holds the longest possible stream, and
+// copies the group's stream words out (zeros past the bits).
+constexpr int kPackWords = (int)(tans_pack::max_stream_bytes(tans_pack::kMaxSteps) / 4);
+
+__global__ __launch_bounds__(kEncBlock) void enc_place_packed_kernel(
+    const uint16_t* __restrict__ chunks, const uint16_t* __restrict__ pstate,
+    const uint16_t* __restrict__ plen, int64_t K, int64_t S, uint32_t L,
+    const int64_t* __restrict__ offsets, uint32_t* __restrict__ comp) {
+    __shared__ uint32_t bufs[kEncBlock / kLanes][kPackWords];
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int wave = threadIdx.x / kLanes;
+    const int64_t g = (int64_t)blockIdx.x * (kEncBlock / kLanes) + wave;
+    const int64_t G = (K + kLanes - 1) / kLanes;
+    if (g >= G) return;
+    uint32_t* b = bufs[wave];
+    for (int i = lane; i < kPackWords; i += kLanes) b[i] = 0u;
+    const int64_t k = g * kLanes + lane;
+    const bool active = k < K;
+    const uint32_t len = active ? plen[k] : 0u;
+    const uint32_t cnt = len + (uint32_t)__shfl_xor((int)len, 1, kLanes);   // the pair's bits
+    uint32_t v = (lane & 1) ? 0u : cnt;
+    #pragma unroll
+    for (int d = 1; d < kLanes; d <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)v, d, kLanes);
+        if (lane >= d) v += y;
+    }
+    const int hb = tans_pack::hdr_bytes(S);
+    const uint32_t end = (uint32_t)tans_pack::hdr_total(S) * 8u + v;
+    const uint32_t start = end - cnt;
+    // (the wave's LDS accesses execute in order: the zeroing above lands first)
+    if (!(lane & 1)) {
+        const uint32_t at = (uint32_t)(lane >> 1) * (uint32_t)hb;
+        atomicOr(&b[at >> 2], cnt << (8u * (at & 3u)));
+    }
+    if (active) {
+        const bool odd = lane & 1;
+        uint32_t o = 0;   // bits of the lane placed so far
+        auto put = [&](uint32_t val, uint32_t nb) {
+            if (nb == 0) return;
+            // odd lanes: the field's bits run backwards, so it sits reversed
+            // at [end - o - nb, end - o)
+            const uint32_t p = odd ? end - o - nb : start + o;
+            const uint32_t f = odd ? __builtin_bitreverse32(val) >> (32u - nb) : val;
+            const uint32_t sh = p & 31u;
+            atomicOr(&b[p >> 5], f << sh);
+            if (sh + nb > 32u) atomicOr(&b[(p >> 5) + 1], f >> (32u - sh));
+            o += nb;
+        };
+        put((uint32_t)pstate[k] - L, (uint32_t)tans_pack::kStateBits);
+        for (int64_t s = 0; s < S; s++) {
+            const uint32_t c = chunks[s * K + k];
+            put(c & 0xFFFu, c >> 12);
+        }
+    }
+    const int64_t base = offsets[g];
+    const int64_t glen = offsets[g + 1] - base;
+    for (int64_t i = lane; i < glen && i < kPackWords; i += kLanes) comp[base + i] = b[i];
+}
+
 // Sign/mantissa tiles: sm[(t K + k) * 8] from bytes [16t, 16t + 16) of row
 // k (zero past N).  A workgroup of 4 waves takes 32 rows x 64 tiles: each
 // wave reads 8 rows, one row segment of 1 KiB per instruction (lane = tile),
@@ -517,13 +604,20 @@ int tans_gpu_encode_workspace(int64_t K, int64_t N, int32_t log2L, int64_t* work
     return TANS_OK;
 }
 
-int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t* enc_tab,
-                          const uint16_t* enc_next, int32_t log2L, void* workspace,
-                          int64_t workspace_bytes, int64_t* offsets, uint16_t* states, void* sm,
-                          int32_t* status, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// begin of both layouts; packed: states == NULL (the workspace keeps them)
+int gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t* enc_tab,
+                     const uint16_t* enc_next, int32_t log2L, void* workspace,
+                     int64_t workspace_bytes, int64_t* offsets, uint16_t* states, void* sm,
+                     int32_t* status, void* stream, bool packed) {
     int64_t need = 0;
     int rc = tans_gpu_encode_workspace(K, N, log2L, &need);
     if (rc) return rc;
+    if (packed && (log2L != TANS_PAIR_LOG2L || N > 2 * tans_pack::kMaxSteps))
+        return fail(TANS_EINVAL, "gpu_encode_packed: needs log2L 12 and N <= 64");
     if (K == 0 || N == 0) {
         if (K == 0 && offsets) {   // offsets = {0}
             hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(kEncBlock), 0, (hipStream_t)stream,
@@ -532,7 +626,8 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
         }
         return fail(TANS_EINVAL, "gpu_encode: N must be positive when K > 0");
     }
-    if (!fp8 || !enc_tab || !enc_next || !workspace || !offsets || !states || !sm || !status)
+    if (!fp8 || !enc_tab || !enc_next || !workspace || !offsets || (!states && !packed) || !sm ||
+        !status)
         return fail(TANS_EINVAL, "gpu_encode: null pointer");
     if (workspace_bytes < need) return fail(TANS_EINVAL, "gpu_encode: workspace too small");
     if (reinterpret_cast<uintptr_t>(fp8) % 16)
@@ -550,16 +645,22 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
     char* ws = static_cast<char*>(workspace);
     uint16_t* chunks = reinterpret_cast<uint16_t*>(ws + l.chunks);
     uint32_t* glen = reinterpret_cast<uint32_t*>(ws + l.glen);
+    uint16_t* plen = reinterpret_cast<uint16_t*>(ws + l.plen);
     hipStream_t st = (hipStream_t)stream;
     const unsigned lane_blocks = (unsigned)((K + kEncBlock - 1) / kEncBlock);
-    if (sps == 2)
+    if (packed)
+        hipLaunchKernelGGL((enc_backward_kernel<2, true>), dim3(lane_blocks), dim3(kEncBlock), 0,
+                           st, (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
+                           reinterpret_cast<uint16_t*>(ws + l.pstate), glen, (uint32_t*)sm,
+                           status, plen);
+    else if (sps == 2)
         hipLaunchKernelGGL(enc_backward_kernel<2>, dim3(lane_blocks), dim3(kEncBlock), 0, st,
                            (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
-                           states, glen, (uint32_t*)sm, status);
+                           states, glen, (uint32_t*)sm, status, plen);
     else
         hipLaunchKernelGGL(enc_backward_kernel<1>, dim3(lane_blocks), dim3(kEncBlock), 0, st,
                            (const uint8_t*)fp8, K, N, enc_tab, enc_next, (int)log2L, chunks,
-                           states, glen, (uint32_t*)sm, status);
+                           states, glen, (uint32_t*)sm, status, plen);
     if ((rc = hip_check(hipGetLastError(), "enc_backward_kernel launch"))) return rc;
     hipLaunchKernelGGL(enc_scan_kernel, dim3(1), dim3(1024), 0, st, glen, G, offsets);
     if ((rc = hip_check(hipGetLastError(), "enc_scan_kernel launch"))) return rc;
@@ -569,11 +670,14 @@ int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t*
     return hip_check(hipGetLastError(), "enc_sm_kernel launch");
 }
 
-int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* workspace,
-                           const int64_t* offsets, void* comp, int64_t comp_bytes, void* stream) {
+int gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* workspace,
+                      const int64_t* offsets, void* comp, int64_t comp_bytes, void* stream,
+                      bool packed) {
     int64_t need = 0;
     int rc = tans_gpu_encode_workspace(K, N, log2L, &need);
     if (rc) return rc;
+    if (packed && (log2L != TANS_PAIR_LOG2L || N > 2 * tans_pack::kMaxSteps))
+        return fail(TANS_EINVAL, "gpu_encode_packed: needs log2L 12 and N <= 64");
     if (!workspace || !offsets || !comp) return fail(TANS_EINVAL, "gpu_encode: null pointer");
     if (comp_bytes < kTailWords * 4 || comp_bytes % 4)
         return fail(TANS_EINVAL, "gpu_encode: comp must hold the stream words and the 1 KiB tail");
@@ -588,7 +692,12 @@ int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* work
         const char* ws = static_cast<const char*>(workspace);
         const dim3 grid((unsigned)((G + kEncBlock / kLanes - 1) / (kEncBlock / kLanes)));
         const uint16_t* ch = reinterpret_cast<const uint16_t*>(ws + l.chunks);
-        if (sps == 1)   // 2^11-state tables: the 3-3-2 schedule
+        if (packed)
+            hipLaunchKernelGGL(enc_place_packed_kernel, grid, dim3(kEncBlock), 0, st, ch,
+                               reinterpret_cast<const uint16_t*>(ws + l.pstate),
+                               reinterpret_cast<const uint16_t*>(ws + l.plen), K, S,
+                               (uint32_t)(1u << log2L), offsets, c32);
+        else if (sps == 1)   // 2^11-state tables: the 3-3-2 schedule
             hipLaunchKernelGGL(enc_place_kernel<true>, grid, dim3(kEncBlock), 0, st, ch, K, S,
                                offsets, c32);
         else
@@ -599,6 +708,37 @@ int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* work
     hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((kTailWords + kEncBlock - 1) / kEncBlock)),
                        dim3(kEncBlock), 0, st, c32 + words_total, kTailWords);
     return hip_check(hipGetLastError(), "gpu_encode tail");
+}
+
+}  // namespace
+
+extern "C" {
+
+int tans_gpu_encode_begin(const void* fp8, int64_t K, int64_t N, const uint32_t* enc_tab,
+                          const uint16_t* enc_next, int32_t log2L, void* workspace,
+                          int64_t workspace_bytes, int64_t* offsets, uint16_t* states, void* sm,
+                          int32_t* status, void* stream) {
+    return gpu_encode_begin(fp8, K, N, enc_tab, enc_next, log2L, workspace, workspace_bytes,
+                            offsets, states, sm, status, stream, false);
+}
+
+int tans_gpu_encode_finish(int64_t K, int64_t N, int32_t log2L, const void* workspace,
+                           const int64_t* offsets, void* comp, int64_t comp_bytes, void* stream) {
+    return gpu_encode_finish(K, N, log2L, workspace, offsets, comp, comp_bytes, stream, false);
+}
+
+int tans_gpu_encode_packed_begin(const void* fp8, int64_t K, int64_t N, const uint32_t* enc_tab,
+                                 const uint16_t* enc_next, int32_t log2L, void* workspace,
+                                 int64_t workspace_bytes, int64_t* offsets, void* sm,
+                                 int32_t* status, void* stream) {
+    return gpu_encode_begin(fp8, K, N, enc_tab, enc_next, log2L, workspace, workspace_bytes,
+                            offsets, nullptr, sm, status, stream, true);
+}
+
+int tans_gpu_encode_packed_finish(int64_t K, int64_t N, int32_t log2L, const void* workspace,
+                                  const int64_t* offsets, void* comp, int64_t comp_bytes,
+                                  void* stream) {
+    return gpu_encode_finish(K, N, log2L, workspace, offsets, comp, comp_bytes, stream, true);
 }
 
 }  // extern "C"

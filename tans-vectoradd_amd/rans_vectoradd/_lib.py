@@ -33,6 +33,8 @@ EXPORTS = (
     "tans_gpu_encode_workspace",
     "tans_gpu_encode_begin",
     "tans_gpu_encode_finish",
+    "tans_gpu_encode_packed_begin",
+    "tans_gpu_encode_packed_finish",
 )
 
 TANS_LANES = 64
@@ -80,6 +82,8 @@ for _name, _args in {
     "tans_gpu_encode_workspace": [_I64, _I64, _I32, ctypes.POINTER(_I64)],
     "tans_gpu_encode_begin": [_P, _I64, _I64, _P, _P, _I32, _P, _I64, _P, _P, _P, _P, _P],
     "tans_gpu_encode_finish": [_I64, _I64, _I32, _P, _P, _P, _I64, _P],
+    "tans_gpu_encode_packed_begin": [_P, _I64, _I64, _P, _P, _I32, _P, _I64, _P, _P, _P, _P],
+    "tans_gpu_encode_packed_finish": [_I64, _I64, _I32, _P, _P, _P, _I64, _P],
 }.items():
     getattr(lib, _name).restype = ctypes.c_int
     getattr(lib, _name).argtypes = _args

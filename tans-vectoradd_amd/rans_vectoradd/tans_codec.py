@@ -343,9 +343,9 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
         wp[:R, :C] = w
         w = wp
     slab = gemm_slab(w, S, Nc)
-    # the GEMM kernel reads the refill-schedule layout (encode_gpu's only one)
+    # the GEMM kernel reads the refill-schedule layout
     if slab.is_cuda:
-        enc = encode_gpu(slab, exp_freqs, alphabet=alphabet)
+        enc = encode_gpu(slab, exp_freqs, alphabet=alphabet, layout="words")
     else:
         enc = encode(slab, exp_freqs, alphabet=alphabet, layout="words")
     comp, states, offsets, partial, sm, freqs, spread = enc
@@ -354,7 +354,7 @@ def encode_matrix(w_fp8: torch.Tensor, exp_freqs, *, segments: int | None = None
 
 
 # ---------------------------------------------------------------------------
-# GPU encoder (the bytes of encode(..., layout="words"), from FP8 bytes on the device)
+# GPU encoder (the same bytes as encode(), from FP8 bytes on the device)
 # ---------------------------------------------------------------------------
 
 _ENC_TABLES: dict = {}
@@ -393,12 +393,13 @@ def _encode_tables(exp_freqs, alphabet: str, dev: torch.device):
     return _ENC_TABLES[key]
 
 
-def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair"):
+def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: str = "pair",
+               layout: str = "auto"):
     """encode() on the GPU: FP8 bytes [K, N] (uint8, on a GPU, N even) ->
-    the 7-tuple of encode(..., layout="words") with the same bytes, as
+    the 7-tuple of encode() with the same arguments, byte for byte, as
     device tensors (freqs and spread included, ready for gpu_tans_decode).
-    It writes the refill-schedule layout only, which every decoder reads at
-    any N.  Reads the stream length
+    ``layout`` as in encode(): the packed layout of short streams by
+    default where it applies (pair alphabet, N <= 64; states empty).  Reads the stream length
     back from the device once (the size of the compressed tensor)."""
     if not (isinstance(fp8_bytes, torch.Tensor) and fp8_bytes.dim() == 2
             and fp8_bytes.dtype == torch.uint8):
@@ -411,6 +412,7 @@ def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: s
     if N % 2:
         raise ValueError("N must be even")
     _check_tile(tile, N)
+    packed = packed_layout(N, alphabet, layout)
     if isinstance(exp_freqs, torch.Tensor):
         exp_freqs = exp_freqs.detach().cpu().float().numpy()
     nsym, L, _ = ALPHABETS[alphabet]
@@ -426,20 +428,27 @@ def encode_gpu(fp8_bytes: torch.Tensor, exp_freqs, tile: int = 0, *, alphabet: s
         check(lib.tans_gpu_encode_workspace(K, N, log2L, ctypes.byref(ws_bytes)), "encode_gpu")
         ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=dev)
         offsets = torch.empty(G + 1, dtype=torch.int64, device=dev)
-        states = torch.empty(K, dtype=torch.uint16, device=dev)
+        states = torch.empty(0 if packed else K, dtype=torch.uint16, device=dev)
         sm = torch.empty(((N + 15) // 16, K, 8), dtype=torch.uint8, device=dev)
         status = torch.zeros(1, dtype=torch.int32, device=dev)
         stream = torch.cuda.current_stream(dev).cuda_stream
-        check(lib.tans_gpu_encode_begin(x.data_ptr(), K, N, tab_d.data_ptr(), next_d.data_ptr(),
-                                        log2L, ws.data_ptr(), ws.numel(), offsets.data_ptr(),
-                                        states.data_ptr(), sm.data_ptr(), status.data_ptr(),
-                                        stream), "encode_gpu")
+        if packed and K:
+            check(lib.tans_gpu_encode_packed_begin(
+                x.data_ptr(), K, N, tab_d.data_ptr(), next_d.data_ptr(), log2L, ws.data_ptr(),
+                ws.numel(), offsets.data_ptr(), sm.data_ptr(), status.data_ptr(), stream),
+                "encode_gpu")
+        else:
+            check(lib.tans_gpu_encode_begin(
+                x.data_ptr(), K, N, tab_d.data_ptr(), next_d.data_ptr(), log2L, ws.data_ptr(),
+                ws.numel(), offsets.data_ptr(), states.data_ptr(), sm.data_ptr(),
+                status.data_ptr(), stream), "encode_gpu")
         total, bad = (int(v) for v in torch.stack([offsets[G], status[0].to(torch.int64)]).tolist())
         if bad:
             raise RuntimeError("encode_gpu: data holds a symbol whose frequency is 0")
         comp = torch.empty((total + 256) * 4, dtype=torch.uint8, device=dev)
-        check(lib.tans_gpu_encode_finish(K, N, log2L, ws.data_ptr(), offsets.data_ptr(),
-                                         comp.data_ptr(), comp.numel(), stream), "encode_gpu")
+        finish = lib.tans_gpu_encode_packed_finish if packed and K else lib.tans_gpu_encode_finish
+        check(finish(K, N, log2L, ws.data_ptr(), offsets.data_ptr(), comp.data_ptr(),
+                     comp.numel(), stream), "encode_gpu")
     partial = torch.empty(0, dtype=torch.uint8, device=dev)
     return (comp, states, offsets, partial, sm, torch.from_numpy(freqs.copy()).to(dev),
             torch.from_numpy(spread.copy()).to(dev))

@@ -21,10 +21,9 @@ def R():
     return rans_vectoradd
 
 
-def _compare(T, fp8, hist, alphabet):
-    # the GPU encoder writes the refill-schedule layout at every N
-    cpu = T.encode(fp8, hist, alphabet=alphabet, layout="words")
-    gpu = T.encode_gpu(fp8.cuda(), hist, alphabet=alphabet)
+def _compare(T, fp8, hist, alphabet, layout="auto"):
+    cpu = T.encode(fp8, hist, alphabet=alphabet, layout=layout)
+    gpu = T.encode_gpu(fp8.cuda(), hist, alphabet=alphabet, layout=layout)
     names = ("comp", "states", "offsets", "partial", "sm", "freqs", "spread")
     for name, c, g in zip(names, cpu, gpu):
         assert g.is_cuda, name
@@ -32,12 +31,17 @@ def _compare(T, fp8, hist, alphabet):
     return gpu
 
 
-@pytest.mark.parametrize("alphabet", ALPHABETS)
-@pytest.mark.parametrize("K,N", [(128, 128), (1024, 128), (10000, 128), (100000, 128),
-                                 (64, 2), (65, 18), (200, 130), (3, 1000), (1, 16),
-                                 (127, 4096), (130, 30), (4096, 14), (300, 208), (70, 48),
-                                 (2000, 20), (2000, 36), (1000, 34)])
-def test_gpu_encode_matches_cpu(R, alphabet, K, N):
+SHAPES = [(128, 128), (1024, 128), (10000, 128), (100000, 128), (64, 2), (65, 18), (200, 130),
+          (3, 1000), (1, 16), (127, 4096), (130, 30), (4096, 14), (300, 208), (70, 48),
+          (2000, 20), (2000, 36), (1000, 34)]
+# every shape with both alphabets; pair shapes of N <= 64 once more in the
+# refill-schedule layout ("auto" gives them the packed one)
+CASES = ([(a, K, N, "auto") for a in ALPHABETS for K, N in SHAPES]
+         + [("pair", K, N, "words") for K, N in SHAPES if N <= 64])
+
+
+@pytest.mark.parametrize("alphabet,K,N,layout", CASES)
+def test_gpu_encode_matches_cpu(R, alphabet, K, N, layout):
     """N % 16 == 0 takes the backward pass that reads rows in 128-byte blocks
     (whole blocks at N = 128, 4096; a partial last block at 208, 48, 16) and
     writes the sign/mantissa tiles itself; the other widths read one step's
@@ -45,12 +49,13 @@ def test_gpu_encode_matches_cpu(R, alphabet, K, N):
     K < 64 give groups with lanes out of range; N = 2 (pair) is one step.
     N = 18, 20, 34, 36 end in a tile of one refill segment (18, 34 with both
     alphabets, 20, 36 with pairs), where the check before it is the plain
-    one."""
+    one.  With the pair alphabet and N <= 64, layout "auto" is the packed
+    layout of short streams (its own place pass)."""
     from rans_vectoradd import tans_codec as T
-    _say(f"case: encode_gpu K={K} N={N} {alphabet}")
+    _say(f"case: encode_gpu K={K} N={N} {alphabet} {layout}")
     torch.manual_seed(42)
     fp8 = R.random_fp8_bytes(K * N, device="cpu").reshape(K, N)
-    _compare(T, fp8, torch.tensor(R.QWEN3_14B_FP8_EXP), alphabet)
+    _compare(T, fp8, torch.tensor(R.QWEN3_14B_FP8_EXP), alphabet, layout)
 
 
 @pytest.mark.parametrize("alphabet", ALPHABETS)
@@ -65,6 +70,23 @@ def test_gpu_encode_config_data_roundtrip(R, alphabet, dist):
     q, _ = gen(n, seed=9)
     fp8 = q.reshape(n // N, N)
     comp, st, off, part, sm, fr, sp = _compare(T, fp8, D.exp_histogram(q), alphabet)
+    dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
+    assert torch.equal(dec.cpu(), fp8.t())
+
+
+@pytest.mark.parametrize("N", [16, 64, 30])
+def test_gpu_encode_packed_config_data(R, N):
+    """Config-1 data (own histogram) in the packed layout of short streams,
+    2^22 elements at 16, 64 and 30 elements per lane (several rounds of the
+    place pass' workgroups; a ragged last tile at 30): GPU encode == CPU
+    encode, and the GPU decode of it == the input."""
+    from rans_vectoradd import data as D, tans_codec as T
+    _say(f"case: encode_gpu packed 2^22, {N} per lane")
+    K = (1 << 22) // N
+    q, _ = D.gaussian_fp8_bytes(K * N, seed=N)
+    fp8 = q.reshape(K, N)
+    comp, st, off, part, sm, fr, sp = _compare(T, fp8, D.exp_histogram(q), "pair")
+    assert st.numel() == 0
     dec = R.gpu_tans_decode(comp, off, st, part, sm, sp, fr, N)
     assert torch.equal(dec.cpu(), fp8.t())
 
@@ -88,7 +110,7 @@ def test_gpu_encode_edge_cases(R):
     view = big.cuda().reshape(-1)[2:2 + 64 * 34].reshape(64, 34)
     assert view.data_ptr() % 16 != 0
     a = T.encode_gpu(view, exp)
-    b = T.encode(view.cpu().contiguous(), exp, layout="words")
+    b = T.encode(view.cpu().contiguous(), exp)
     assert torch.equal(a[0].cpu(), b[0]) and torch.equal(a[4].cpu(), b[4])
     with pytest.raises(ValueError):
         T.encode_gpu(torch.zeros((4, 16), dtype=torch.uint8), exp)       # CPU tensor
