@@ -1158,7 +1158,37 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             }
         }
     };
+    // Packed streams of one or two tiles: a wave switches groups every tile
+    // or two, so the next group's stream and sign/mantissa tiles are loaded
+    // as soon as the current stream is in LDS, before its tiles are decoded
+    // (the offsets two groups ahead).  The loads are unconditional (a wave
+    // past the last group loads that one again, to no use), so the waits of
+    // the tiles in between count them exactly.
+    constexpr bool PREFETCH = PACKED && -FIRST <= 2;
+    v2u smn[C][PREFETCH ? NSM : 1];   // the next group's sign/mantissa tiles
+    uint32_t plen_n[C];               // and its streams' bytes
+    auto prefetch = [&](int64_t gnext) {
+        if constexpr (PREFETCH) {
+            const int64_t g = gnext < n_groups ? gnext : n_groups - 1;
+            const int64_t k0 = g * kLanes;
+            const uint32_t smb = (uint32_t)(K - k0 < kLanes ? K - k0 : kLanes) * 8u;
+            plen_n[0] = pk_fetch<NSEG>(a_comp, a_words, noff_lane(0), noff_lane(1), lane,
+                                       first[0]);
+            plen_n[1] = pk_fetch<NSEG>(b_comp, b_words, noff_lane(2), noff_lane(3), lane,
+                                       first[1]);
+            const char* rows[2] = {reinterpret_cast<const char*>(a_sm + k0),
+                                   reinterpret_cast<const char*>(b_sm + k0)};
+            #pragma unroll
+            for (int c = 0; c < C; c++)
+                #pragma unroll
+                for (int i = 0; i < NSM; i++)
+                    smn[c][i] = __builtin_amdgcn_raw_buffer_load_b64(
+                        rsrc(rows[c] + (int64_t)i * w.sm_stride, smb), (uint32_t)lane * 8u, 0,
+                        kNT);
+        }
+    };
     setup(g0, false);
+    if constexpr (PREFETCH) next_offsets(g0 + grid_groups);
     table_store<L, PACKED>(tbl, tr);
     if (threadIdx.x == 0) smem.init();
     __syncthreads();
@@ -1174,6 +1204,11 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
                 lane_init(w.ch.l[c], w.ch.f[c], lane, glanes[c / 2], st0[c], L, smem.sink_off());
             }
         }
+        if constexpr (PREFETCH) {
+            static_assert(G == 1, "one group per wave");
+            prefetch(g0 + grid_groups);
+            next_offsets(g0 + 2 * grid_groups);
+        }
         w.base = done;
         // the first n_tiles - 1 tiles four per iteration, then the last one,
         // which ends the streams (its variant chosen by tile mod 4)
@@ -1185,7 +1220,7 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
             if (t + 3 < body) w.template tile<3, false>(t + 3);
         }
         static_assert(kSmAhead == 4, "the loop above is unrolled for kSmAhead == 4");
-        if constexpr (AHEAD) next_offsets(g0 + grid_groups);
+        if constexpr (AHEAD && !PREFETCH) next_offsets(g0 + grid_groups);
         switch (body % kSmAhead) {
             case 0: w.template tile<0, true>(body); break;
             case 1: w.template tile<1, true>(body); break;
@@ -1195,7 +1230,21 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
         done += n_tiles;
         g0 += grid_groups;
         if (g0 >= n_groups) break;
-        setup(g0, AHEAD);
+        if constexpr (PREFETCH) {   // the group prefetched above becomes the current one
+            const int64_t k0 = g0 * kLanes;
+            const int lanes = K - k0 < kLanes ? (int)(K - k0) : kLanes;
+            w.sm_bytes[0] = (uint32_t)lanes * 8u;
+            w.out_cur[0] = reinterpret_cast<char*>(out + k0);
+            glanes[0] = lanes;
+            #pragma unroll
+            for (int c = 0; c < C; c++) {
+                plen[c] = plen_n[c];
+                #pragma unroll
+                for (int i = 0; i < (PREFETCH ? NSM : 1); i++) w.sm[c][i] = smn[c][i];
+            }
+        } else {
+            setup(g0, AHEAD);
+        }
     }
 }
 
