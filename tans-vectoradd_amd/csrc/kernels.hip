@@ -1164,8 +1164,11 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
     // (the offsets two groups ahead).  The loads are unconditional (a wave
     // past the last group loads that one again, to no use), so the waits of
     // the tiles in between count them exactly.
-    constexpr bool PREFETCH = PACKED && -FIRST <= 2;
-    v2u smn[C][PREFETCH ? NSM : 1];   // the next group's sign/mantissa tiles
+    constexpr bool PREFETCH = PACKED && -FIRST == 2;
+    // One-tile streams take the streams two groups ahead (two stream
+    // buffers in turn), the sign/mantissa tiles one group ahead.
+    constexpr bool DEEP = PACKED && -FIRST == 1;
+    v2u smn[C][(PREFETCH || DEEP) ? NSM : 1];   // the next group's sign/mantissa tiles
     uint32_t plen_n[C];               // and its streams' bytes
     auto prefetch = [&](int64_t gnext) {
         if constexpr (PREFETCH) {
@@ -1187,13 +1190,67 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
                         kNT);
         }
     };
+    // the group after g0 becomes the current one (its loads were issued ahead)
+    auto advance = [&]() {
+        const int64_t k0 = g0 * kLanes;
+        const int lanes = K - k0 < kLanes ? (int)(K - k0) : kLanes;
+        w.sm_bytes[0] = (uint32_t)lanes * 8u;
+        w.out_cur[0] = reinterpret_cast<char*>(out + k0);
+        glanes[0] = lanes;
+        #pragma unroll
+        for (int c = 0; c < C; c++)
+            #pragma unroll
+            for (int i = 0; i < ((PREFETCH || DEEP) ? NSM : 1); i++) w.sm[c][i] = smn[c][i];
+    };
+    Seg second[C][DEEP ? kPackMaxSegs : 1];   // DEEP: the second stream buffer
+    uint32_t plen2[C];
     setup(g0, false);
     if constexpr (PREFETCH) next_offsets(g0 + grid_groups);
+    if constexpr (DEEP) {
+        const int64_t g1 = g0 + grid_groups < n_groups ? g0 + grid_groups : n_groups - 1;
+        plen2[0] = pk_fetch<NSEG>(a_comp, a_words, a_off[g1], a_off[g1 + 1], lane, second[0]);
+        plen2[1] = pk_fetch<NSEG>(b_comp, b_words, b_off[g1], b_off[g1 + 1], lane, second[1]);
+        next_offsets(g0 + 2 * grid_groups);
+    }
     table_store<L, PACKED>(tbl, tr);
     if (threadIdx.x == 0) smem.init();
     __syncthreads();
     if (!live) return;
     int done = 0;   // tiles of earlier groups (the pacing count runs on)
+    if constexpr (DEEP) {
+        static_assert(G == 1, "one group per wave");
+        // group g0's stream is in cur: put it in LDS, load group g0 + 2 grid's
+        // into cur, then decode g0; false once the wave has no groups left
+        auto step = [&](Seg (&cur)[C][DEEP ? kPackMaxSegs : 1], uint32_t (&pcur)[C]) -> bool {
+            if constexpr (DEEP) {
+                #pragma unroll
+                for (int c = 0; c < C; c++)
+                    pk_start<1, NSEG>(w.pk[c], w.preg[c], lane, cur[c], pcur[c]);
+                pcur[0] = pk_fetch<NSEG>(a_comp, a_words, noff_lane(0), noff_lane(1), lane, cur[0]);
+                pcur[1] = pk_fetch<NSEG>(b_comp, b_words, noff_lane(2), noff_lane(3), lane, cur[1]);
+                next_offsets(g0 + 3 * grid_groups);
+                const int64_t gn = g0 + grid_groups < n_groups ? g0 + grid_groups : n_groups - 1;
+                const int64_t kn = gn * kLanes;
+                const uint32_t smb = (uint32_t)(K - kn < kLanes ? K - kn : kLanes) * 8u;
+                smn[0][0] = __builtin_amdgcn_raw_buffer_load_b64(
+                    rsrc(reinterpret_cast<const char*>(a_sm + kn), smb), (uint32_t)lane * 8u, 0, kNT);
+                smn[1][0] = __builtin_amdgcn_raw_buffer_load_b64(
+                    rsrc(reinterpret_cast<const char*>(b_sm + kn), smb), (uint32_t)lane * 8u, 0, kNT);
+                w.base = done;
+                w.template tile<0, true>(0);
+                done += 1;
+                g0 += grid_groups;
+                if (g0 >= n_groups) return false;
+                advance();
+            }
+            return true;
+        };
+        for (;;) {
+            if (!step(first, plen)) break;
+            if (!step(second, plen2)) break;
+        }
+        return;
+    }
     for (;;) {
         #pragma unroll
         for (int c = 0; c < C; c++) {
@@ -1231,17 +1288,9 @@ __global__ __launch_bounds__(kDecBlock) void fused_add_kernel(
         g0 += grid_groups;
         if (g0 >= n_groups) break;
         if constexpr (PREFETCH) {   // the group prefetched above becomes the current one
-            const int64_t k0 = g0 * kLanes;
-            const int lanes = K - k0 < kLanes ? (int)(K - k0) : kLanes;
-            w.sm_bytes[0] = (uint32_t)lanes * 8u;
-            w.out_cur[0] = reinterpret_cast<char*>(out + k0);
-            glanes[0] = lanes;
+            advance();
             #pragma unroll
-            for (int c = 0; c < C; c++) {
-                plen[c] = plen_n[c];
-                #pragma unroll
-                for (int i = 0; i < (PREFETCH ? NSM : 1); i++) w.sm[c][i] = smn[c][i];
-            }
+            for (int c = 0; c < C; c++) plen[c] = plen_n[c];
         } else {
             setup(g0, AHEAD);
         }
