@@ -17,7 +17,8 @@
 //                            matrix cores (no counterpart in the
 //                            reference), with gemm_finalize_kernel and the
 //                            uncompressed baselines gemm_raw_dot2_kernel
-//                            (B = 1) and gemm_raw_kernel (B >= 2)
+//                            (B = 1), gemm_raw_xs_kernel (B >= 2, rows of
+//                            up to 8192 columns) and gemm_raw_kernel
 //
 // Decoder design.  One wave64 decodes one 64-lane group; each lane owns one
 // tANS state.  The decode table lives in LDS as 8-byte entries addressed by
@@ -2123,6 +2124,151 @@ __global__ __launch_bounds__(kRawMaxWaves * kLanes) void gemm_raw_kernel(
     }
 }
 
+// The same products with x held in registers (B >= 2, rows of at most
+// kXsMaxChunks chunks: 8192 columns).  Lanes, blocks and chunks as in
+// gemm_raw_kernel.
+// Each wave owns CPW consecutive chunks and loads x for them once, before
+// its loop; it then streams the workgroup's row groups over its chunks,
+// PIPE row groups of loads in flight in PIPE buffers taken in turn.  So the
+// loop issues only W loads, and its waits cover only them.  A row group's
+// 16 blocks are added by two DPP rotations inside each 16-lane row and two
+// lane shuffles across rows; lanes 0-3 store the wave's sums (batch row
+// j = lane) to LDS, and the workgroup adds them at the end in wave order,
+// so results are deterministic.  Out-of-range rows and chunks read zeros
+// through the buffer bound: a lane's offset past the workgroup's last row
+// or its matrix row stays past the bound for every row group it adds.
+constexpr int kXsMaxWaves = 16;
+constexpr int kXsMaxRg = 32;      // row groups of 4 rows per workgroup
+constexpr int kXsMaxChunks = 32;  // chunks of 256 columns per row (16 waves of 2)
+
+// v_permlane16_swap (H32 false) or v_permlane32_swap of a and c, and the sum
+// of the two registers it leaves: rows of 16 lanes (a0 + a1, c0 + c1,
+// a2 + a3, c2 + c3), or halves of 32 (a_lo + a_hi, c_lo + c_hi).  The
+// builtin's result is read through a 64-bit bit cast: indexing its vector
+// type reads the first element twice with this compiler.
+template <bool H32>
+__device__ __forceinline__ float swap_add(float a, float c) {
+    const uint32_t ua = __builtin_bit_cast(uint32_t, a), uc = __builtin_bit_cast(uint32_t, c);
+    uint64_t u;
+    if constexpr (H32) u = __builtin_bit_cast(uint64_t, __builtin_amdgcn_permlane32_swap(ua, uc, false, false));
+    else u = __builtin_bit_cast(uint64_t, __builtin_amdgcn_permlane16_swap(ua, uc, false, false));
+    return __builtin_bit_cast(float, (uint32_t)u) + __builtin_bit_cast(float, (uint32_t)(u >> 32));
+}
+
+template <bool HI, int CPW, int PIPE>
+__global__ __launch_bounds__(kXsMaxWaves * kLanes) void gemm_raw_xs_kernel(
+    const uint8_t* __restrict__ W, int64_t R, int64_t C, const uint16_t* __restrict__ x, int NB,
+    float scale, uint16_t* __restrict__ y, int64_t ldy, int rg_per_block) {
+    constexpr int NP = HI ? 2 : 1;
+    __shared__ float part[kXsMaxWaves][kXsMaxRg][NP][4][4];   // [.][.][.][batch j][row v]
+    const int lane = threadIdx.x & (kLanes - 1);
+    const int wave = threadIdx.x / kLanes;
+    const int nw = blockDim.x / kLanes;
+    const int b = lane >> 2, i = lane & 3;
+    const int64_t rg0 = (int64_t)blockIdx.x * rg_per_block;
+    const int64_t n_rg_all = (R + 3) / 4;
+    const int n_rg = (int)(n_rg_all - rg0 < rg_per_block ? n_rg_all - rg0 : rg_per_block);
+    const int64_t row_end = 4 * (rg0 + n_rg) < R ? 4 * (rg0 + n_rg) : R;
+    const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
+    // the launcher keeps (R + 4 * (rg_per_block + PIPE)) * C below 2^32
+    const uint32_t bound = (uint32_t)(row_end * C);
+    const Rsrc wsrc = rsrc(W, bound);
+    const Rsrc xsrc = rsrc(x, (uint32_t)(NB * C * 2));
+    v4u xr[CPW][NP][2];   // x[i] (and x[i + 4]) at columns 16b .. 16b + 15 of each chunk
+    uint32_t woff[CPW];   // row i of row group 0, the lane's 16 columns of each chunk
+    #pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        const int64_t ch = (int64_t)wave * CPW + j;
+        const int64_t col = ch * kRawChunk + 16 * b;
+        const bool in = ch < n_chunks && col < C;   // C % 16 == 0
+        woff[j] = in ? (uint32_t)((4 * rg0 + i) * C + col) : bound;
+        #pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const uint32_t o = in && i + 4 * p < NB ? (uint32_t)(((i + 4 * p) * C + col) * 2) : kNoSeg;
+            xr[j][p][0] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, o, 0, 0);
+            xr[j][p][1] = __builtin_amdgcn_raw_buffer_load_b128(xsrc, o, 16, 0);
+        }
+    }
+    // Issue order is what the waits count: the x loads, then the row groups
+    // in order.  The loop's wait for row group s then covers x and leaves
+    // the later row groups in flight; without the barriers the compiler
+    // moves loads past each other and the first wait is for all of them.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t rg_bytes = (uint32_t)(4 * C);
+    v4u wb[PIPE][CPW];
+    auto load = [&](int s, v4u (&buf)[CPW]) {   // row group s of the workgroup
+        #pragma unroll
+        for (int j = 0; j < CPW; j++)
+            buf[j] = __builtin_amdgcn_raw_buffer_load_b128(wsrc, woff[j] + (uint32_t)s * rg_bytes,
+                                                           0, kNT);
+    };
+    #pragma unroll
+    for (int p = 0; p < PIPE; p++) {
+        load(p, wb[p]);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // every workgroup has a row group (the launcher sizes the grid so), and
+    // a loop with no zero-trip test keeps the loads above where they are
+    const int n_iter = (n_rg + PIPE - 1) / PIPE;
+    int it = 0;
+    do {
+        static_for<0, PIPE>([&](auto P) {
+            constexpr int q = decltype(P)::value;
+            const int s = it * PIPE + q;
+            v4f acc[NP];
+            #pragma unroll
+            for (int p = 0; p < NP; p++) acc[p] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            #pragma unroll
+            for (int j = 0; j < CPW; j++) {
+                const uint32_t ws[4] = {wb[q][j].x, wb[q][j].y, wb[q][j].z, wb[q][j].w};
+                #pragma unroll
+                for (int k = 0; k < 4; k++) {   // k-step: columns 16b + 4k .. + 3
+                    const v4bf a = fp8x4_to_bf16(ws[k]);
+                    #pragma unroll
+                    for (int p = 0; p < NP; p++) {
+                        const v4u& xv = xr[j][p][k >> 1];
+                        const v2u xk = (k & 1) ? v2u{xv.z, xv.w} : v2u{xv.x, xv.y};
+                        acc[p] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(
+                            a, __builtin_bit_cast(v4bf, xk), acc[p], 0, 0, 0);
+                    }
+                }
+            }
+            load(s + PIPE, wb[q]);
+            #pragma unroll
+            for (int p = 0; p < NP; p++) {
+                float t[4];
+                // blocks 4r .. 4r + 3 of each 16-lane row r (DPP row_ror 4, 8)
+                #pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    t[v] = acc[p][v];
+                    t[v] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                        0, __builtin_bit_cast(int, t[v]), 0x124, 0xF, 0xF, false));
+                    t[v] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                        0, __builtin_bit_cast(int, t[v]), 0x128, 0xF, 0xF, false));
+                }
+                // then the rows: register v's rows 0 + 1 and 2 + 3 paired with
+                // register v + 1's, then the halves, so that row v of the
+                // result holds register v's total (lanes 16v + j: batch row j)
+                const float tot = swap_add<true>(swap_add<false>(t[0], t[1]),
+                                                 swap_add<false>(t[2], t[3]));
+                if (s < n_rg && (lane & 15) < 4) part[wave][s][p][lane & 3][lane >> 4] = tot;
+            }
+        });
+    } while (++it < n_iter);
+    __syncthreads();
+    // outputs (row r of the workgroup, batch row bn), rows consecutive per thread
+    const int rows = (int)(row_end - 4 * rg0);
+    for (int t = threadIdx.x; t < rows * NB; t += blockDim.x) {
+        const int bn = t / rows, r = t % rows;
+        const int s = r / 4, v = r % 4, p = bn / 4, j = bn % 4;
+        float sum = part[0][s][p][j][v];
+        for (int w = 1; w < nw; w++) sum += part[w][s][p][j][v];
+        y[(int64_t)bn * ldy + 4 * rg0 + r] = bf16_rne(sum * scale);
+    }
+}
+
 int fail(int code, const std::string& msg) {
     tans_internal_set_error(msg.c_str());
     return code;
@@ -2512,6 +2658,54 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
         else launch(gemm_raw_dot2_kernel<1, 4>);
         return hip_check(hipGetLastError(), "gemm_raw_dot2_kernel launch");
     }
+    const int cus = cu_count();
+    if (cus <= 0) return fail(TANS_EHIP, "gemm_raw: cannot query the device's CU count");
+    const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
+    if ((int64_t)B * C * 2 > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: rows too long");
+    if (n_chunks <= kXsMaxChunks) {
+        // x in registers: one chunk per wave up to 16 chunks, then two; row
+        // groups split evenly over about one workgroup per CU.  Measured on
+        // 17408 x 5120 (10 waves of 2 chunks) at B = 2 / 4 / 8: 15.7 / 16.3 /
+        // 18.0 us per call, against 19.1 / 20.8 / 25.9 us with gemm_raw_kernel
+        // (4 or 8 row groups in flight: 16.0-17.2 / 16.7-17.7 / 18.8-20.0 us).
+        // Longer rows stay with gemm_raw_kernel: on 5120 x 17408 a wave of
+        // this kernel would hold 9 chunks of x and stream only 5 row groups; it
+        // measured 18.8 / 19.9 / 23.6 against 18.4 / 19.3 / 24.0 us.
+        const int cpw = n_chunks <= 16 ? 1 : 2;
+        const int64_t nw = (n_chunks + cpw - 1) / cpw;
+        const int pipe = cpw == 1 ? 8 : 6;
+        const int64_t n_rg = (R + 3) / 4;
+        const int64_t rgb = std::min<int64_t>(kXsMaxRg, (n_rg + cus - 1) / cus);
+        // launches of at most rows_per_launch rows keep each W slice below
+        // 2^31 bytes; the loads a workgroup issues past its last row reach
+        // at most 4 * (rgb + 2 * pipe) + 4 rows further, so every offset
+        // stays below 2^32
+        const int64_t rows_per_launch =
+            std::max<int64_t>(4 * rgb, INT32_MAX / C / (4 * rgb) * (4 * rgb));
+        if ((4 * (rgb + 2 * pipe) + 4) * C > INT32_MAX)
+            return fail(TANS_EINVAL, "gemm_raw: rows too long");
+        for (int64_t r0 = 0; r0 < R; r0 += rows_per_launch) {
+            const int64_t rl = std::min(rows_per_launch, R - r0);
+            const int64_t blocks = ((rl + 3) / 4 + rgb - 1) / rgb;
+            if (!grid_fits(blocks, kXsMaxWaves * kLanes))
+                return fail(TANS_EINVAL, "gemm_raw: matrix too large");
+            auto launch = [&](auto kernel) {
+                hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3((unsigned)(nw * kLanes)),
+                                   0, st, (const uint8_t*)w + r0 * C, rl, C, (const uint16_t*)x,
+                                   (int)B, scale, (uint16_t*)y + r0, R, (int)rgb);
+            };
+            if (B > 4) {
+                if (cpw == 1) launch(gemm_raw_xs_kernel<true, 1, 8>);
+                else launch(gemm_raw_xs_kernel<true, 2, 6>);
+            } else {
+                if (cpw == 1) launch(gemm_raw_xs_kernel<false, 1, 8>);
+                else launch(gemm_raw_xs_kernel<false, 2, 6>);
+            }
+            const int rc = hip_check(hipGetLastError(), "gemm_raw_xs_kernel launch");
+            if (rc != TANS_OK) return rc;
+        }
+        return TANS_OK;
+    }
     // Workgroups of 4 * kRawGroups rows; their waves split the row's chunks
     // in contiguous ranges.  Up to one workgroup per CU (5120 rows: 256
     // workgroups of 20 rows on MI355X) takes 8 waves each; more workgroups
@@ -2521,10 +2715,7 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
     // 16-row workgroups (320 of them, so 64 CUs held two); on 17408 x 5120:
     // 19.1 / 20.7 / 25.8 against 19.7 / 21.9 / 28.1 us.
     const int64_t rows_wg = 4 * kRawGroups;
-    const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
-    const int cus = cu_count();
-    if (cus <= 0) return fail(TANS_EHIP, "gemm_raw: cannot query the device's CU count");
-    if ((int64_t)B * C * 2 > INT32_MAX || C > INT32_MAX / rows_wg)
+    if (C > INT32_MAX / rows_wg)
         return fail(TANS_EINVAL, "gemm_raw: rows too long");
     // launches of at most rows_per_launch rows keep each W slice below 2^31 bytes
     const int64_t rows_per_launch = std::max<int64_t>(rows_wg, INT32_MAX / C / rows_wg * rows_wg);

@@ -106,13 +106,19 @@ def test_gemm_fused_vector_input_and_determinism(R):
 @pytest.mark.parametrize("rows,cols,B", [(2176, 1280, 1), (2176, 1280, 8), (100, 64, 3),
                                          (5120, 17408 // 4, 2), (5, 16, 2), (33, 48, 8),
                                          (17, 80, 5), (40, 1040, 4), (7, 1040, 1),
-                                         (37, 5136, 1), (9, 10256, 1), (70, 12000, 1)])
+                                         (37, 5136, 1), (9, 10256, 1), (70, 12000, 1),
+                                         (17408, 5120, 8), (1001, 8176, 3), (403, 4112, 8),
+                                         (40003, 2048, 6), (6, 8192, 2), (130, 8208, 8)])
 def test_gemm_raw_vs_float64(R, rows, cols, B):
-    """Both raw kernels (row-streaming at B = 1, matrix cores from B = 2),
-    including rows not a multiple of 16 (the last workgroup's rows past R)
-    and widths not a multiple of 256 (a partial last chunk).  At B = 1 rows
-    of 5120 columns or more are split over 2 waves, of 10240 or more over 4
-    (uneven splits at 5136, 10256 and 12000 columns)."""
+    """The raw kernels: row-streaming at B = 1; from B = 2 x held in
+    registers for rows of up to 8192 columns (one 256-column chunk per wave
+    up to 16 chunks, then two: 4112 columns give 9 waves, the last with one
+    chunk in range; 8176 a partial last chunk), and x loaded per chunk for
+    longer rows (8208 columns here, 17408 in the config-4 tests).  Rows not
+    a multiple of 4 or of the row groups in flight, more workgroups than
+    CUs (40003 rows), widths not a multiple of 256.  At B = 1 rows of 5120
+    columns or more are split over 2 waves, of 10240 or more over 4 (uneven
+    splits at 5136, 10256 and 12000 columns)."""
     _say(f"case: fp8_gemm_raw {rows}x{cols} B={B}")
     w, scale = _weights(rows, cols, seed=7)
     x = _x(B, cols, seed=8)
@@ -121,19 +127,20 @@ def test_gemm_raw_vs_float64(R, rows, cols, B):
 
 
 @pytest.mark.parametrize("B", [3, 8])
-def test_gemm_raw_several_launches(R, B):
-    """A W above 2^31 bytes (131077 x 16400): the raw kernel's launcher
-    splits the rows into launches that each address less than 2^31 bytes
-    (130944 rows, then 133).  Rows at the start, around the split and at
-    the end are checked against float64."""
-    rows, cols = 131077, 16400
+@pytest.mark.parametrize("rows,cols,split", [(131077, 16400, 130944), (262147, 8192, 262016)])
+def test_gemm_raw_several_launches(R, B, rows, cols, split):
+    """A W above 2^31 bytes: the raw kernels' launchers split the rows into
+    launches that each address less than 2^31 bytes (131077 x 16400, x
+    loaded per chunk: 130944 rows, then 133; 262147 x 8192, x in registers:
+    262016 rows, then 131).  Rows at the start, around the split and at the
+    end are checked against float64."""
     _say(f"case: fp8_gemm_raw {rows}x{cols} B={B} (two launches)")
     g = torch.Generator(device="cuda").manual_seed(B)
     w = torch.randint(0, 256, (rows, cols), dtype=torch.uint8, device="cuda", generator=g)
     w = torch.where((w & 0x7F) == 0x7F, torch.zeros_like(w), w)     # no NaN bytes
     x = _x(B, cols, seed=B + 5).cuda()
     y = R.fp8_gemm_raw(w, x, 0.5)
-    for lo, hi in ((0, 64), (130900, 131000), (rows - 64, rows)):
+    for lo, hi in ((0, 64), (split - 100, split + 100), (rows - 64, rows)):
         ref = _reference(w[lo:hi].cpu(), x.cpu(), 0.5)
         _check(y[:, lo:hi], ref)
     del w
