@@ -16,9 +16,10 @@
 //   gemm_fused_kernel<SPS>   decode W + skinny GEMM partial sums on the
 //                            matrix cores (no counterpart in the
 //                            reference), with gemm_finalize_kernel and the
-//                            uncompressed baselines gemm_raw_dot2_kernel
-//                            (B = 1), gemm_raw_xs_kernel (B >= 2, rows of
-//                            up to 8192 columns) and gemm_raw_kernel
+//                            uncompressed baselines gemm_raw_xs_kernel
+//                            (rows of up to 8192 columns), and for longer
+//                            rows gemm_raw_dot2_kernel (B = 1) and
+//                            gemm_raw_kernel (B >= 2)
 //
 // Decoder design.  One wave64 decodes one 64-lane group; each lane owns one
 // tANS state.  The decode table lives in LDS as 8-byte entries addressed by
@@ -1889,13 +1890,14 @@ __global__ __launch_bounds__(kFinWaves * kLanes) void gemm_finalize_kernel(
 }
 
 
-// Uncompressed FP8 GEMV, B = 1 (the baseline of the fused one there): a
+// Uncompressed FP8 GEMV, B = 1, for rows of more than 8192 columns (the
+// baseline of the fused one there; shorter rows take gemm_raw_xs_kernel): a
 // wave takes 4 rows; each lane walks 16-column blocks, so a wave's load is
 // 1 KiB of one row, converting W to bf16 pairs and accumulating
 // v_dot2_f32_bf16 against x read from global memory (cache-resident), then
 // the wave sums its lanes.  C % 16 == 0.  At one batch row its whole-row
-// loads stream W faster than the matrix-core kernel below (17 against 22 us
-// for 17408 x 5120); from two rows on the matrix-core kernel is faster.
+// loads stream W faster than gemm_raw_kernel (17 against 22 us for
+// 17408 x 5120); from two rows on gemm_raw_kernel is faster.
 constexpr int kRawRows = 4;
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -2124,9 +2126,9 @@ __global__ __launch_bounds__(kRawMaxWaves * kLanes) void gemm_raw_kernel(
     }
 }
 
-// The same products with x held in registers (B >= 2, rows of at most
-// kXsMaxChunks chunks: 8192 columns).  Lanes, blocks and chunks as in
-// gemm_raw_kernel.
+// The same products with x held in registers (rows of at most kXsMaxChunks
+// chunks: 8192 columns; every B, lanes j >= B hold zeros).  Lanes, blocks
+// and chunks as in gemm_raw_kernel.
 // Each wave owns CPW consecutive chunks and loads x for them once, before
 // its loop; it then streams the workgroup's row groups over its chunks,
 // PIPE row groups of loads in flight in PIPE buffers taken in turn.  So the
@@ -2641,11 +2643,12 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
     if (!aligned(w, 16) || !aligned(x, 16) || !aligned(y, 2))
         return fail(TANS_EINVAL, "gemm_raw: W and x must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
-    if (B == 1) {
-        // split each row over 2 or 4 waves, about 2.5 KiB or more of it each
-        // (17408 x 5120: 2 waves, 16.4 against 17.2 us per call on MI355X;
-        // 5120 x 17408: 4 waves, 17.4 against 24.1 us)
-        const int ks = C >= 10240 ? 4 : C >= 5120 ? 2 : 1;
+    const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
+    if (B == 1 && n_chunks > kXsMaxChunks) {
+        // rows of more than 8192 columns: the row-streaming kernel, each row
+        // split over 2 or 4 waves, about 2.5 KiB or more of it each
+        // (5120 x 17408: 4 waves, 17.4 against 24.1 us per call on MI355X)
+        const int ks = C >= 10240 ? 4 : 2;
         const int64_t rows_per_block = (256 / kLanes) / ks * kRawRows;
         const int64_t blocks = (R + rows_per_block - 1) / rows_per_block;
         if (!grid_fits(blocks, 256)) return fail(TANS_EINVAL, "gemm_raw: matrix too large");
@@ -2653,21 +2656,20 @@ int tans_fp8_gemm_raw(const void* w, int64_t R, int64_t C, const void* x, int64_
             hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(256), 0, st, (const v4u*)w, R,
                                C, (const v4u*)x, scale, (uint16_t*)y);
         };
-        if (ks == 1) launch(gemm_raw_dot2_kernel<1, 1>);
-        else if (ks == 2) launch(gemm_raw_dot2_kernel<1, 2>);
+        if (ks == 2) launch(gemm_raw_dot2_kernel<1, 2>);
         else launch(gemm_raw_dot2_kernel<1, 4>);
         return hip_check(hipGetLastError(), "gemm_raw_dot2_kernel launch");
     }
     const int cus = cu_count();
     if (cus <= 0) return fail(TANS_EHIP, "gemm_raw: cannot query the device's CU count");
-    const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
     if ((int64_t)B * C * 2 > INT32_MAX) return fail(TANS_EINVAL, "gemm_raw: rows too long");
     if (n_chunks <= kXsMaxChunks) {
         // x in registers: one chunk per wave up to 16 chunks, then two; row
         // groups split evenly over about one workgroup per CU.  Measured on
         // 17408 x 5120 (10 waves of 2 chunks) at B = 2 / 4 / 8: 15.7 / 16.3 /
         // 18.0 us per call, against 19.1 / 20.8 / 25.9 us with gemm_raw_kernel
-        // (4 or 8 row groups in flight: 16.0-17.2 / 16.7-17.7 / 18.8-20.0 us).
+        // (4 or 8 row groups in flight: 16.0-17.2 / 16.7-17.7 / 18.8-20.0 us);
+        // at B = 1 15.6 us against 16.4 us with gemm_raw_dot2_kernel.
         // Longer rows stay with gemm_raw_kernel: on 5120 x 17408 a wave of
         // this kernel would hold 9 chunks of x and stream only 5 row groups; it
         // measured 18.8 / 19.9 / 23.6 against 18.4 / 19.3 / 24.0 us.

@@ -108,17 +108,18 @@ def test_gemm_fused_vector_input_and_determinism(R):
                                          (17, 80, 5), (40, 1040, 4), (7, 1040, 1),
                                          (37, 5136, 1), (9, 10256, 1), (70, 12000, 1),
                                          (17408, 5120, 8), (1001, 8176, 3), (403, 4112, 8),
-                                         (40003, 2048, 6), (6, 8192, 2), (130, 8208, 8)])
+                                         (40003, 2048, 6), (6, 8192, 2), (130, 8208, 8),
+                                         (37, 9008, 1)])
 def test_gemm_raw_vs_float64(R, rows, cols, B):
-    """The raw kernels: row-streaming at B = 1; from B = 2 x held in
-    registers for rows of up to 8192 columns (one 256-column chunk per wave
-    up to 16 chunks, then two: 4112 columns give 9 waves, the last with one
-    chunk in range; 8176 a partial last chunk), and x loaded per chunk for
-    longer rows (8208 columns here, 17408 in the config-4 tests).  Rows not
-    a multiple of 4 or of the row groups in flight, more workgroups than
-    CUs (40003 rows), widths not a multiple of 256.  At B = 1 rows of 5120
-    columns or more are split over 2 waves, of 10240 or more over 4 (uneven
-    splits at 5136, 10256 and 12000 columns)."""
+    """The raw kernels: x held in registers for rows of up to 8192 columns
+    at every B (one 256-column chunk per wave up to 16 chunks, then two:
+    4112 columns give 9 waves, the last with one chunk in range; 8176 a
+    partial last chunk); longer rows row-streaming at B = 1 and with x
+    loaded per chunk from B = 2 (8208 columns here, 17408 in the config-4
+    tests).  Rows not a multiple of 4 or of the row groups in flight, more
+    workgroups than CUs (40003 rows), widths not a multiple of 256.  At
+    B = 1 rows of more than 8192 columns are split over 2 waves, of 10240 or
+    more over 4 (uneven splits at 9008, 10256 and 12000 columns)."""
     _say(f"case: fp8_gemm_raw {rows}x{cols} B={B}")
     w, scale = _weights(rows, cols, seed=7)
     x = _x(B, cols, seed=8)
