@@ -2133,10 +2133,10 @@ __global__ __launch_bounds__(kRawMaxWaves * kLanes) void gemm_raw_kernel(
 // its loop; it then streams the workgroup's row groups over its chunks,
 // PIPE row groups of loads in flight in PIPE buffers taken in turn.  So the
 // loop issues only W loads, and its waits cover only them.  A row group's
-// 16 blocks are added by two DPP rotations inside each 16-lane row and two
-// lane shuffles across rows; lanes 0-3 store the wave's sums (batch row
-// j = lane) to LDS, and the workgroup adds them at the end in wave order,
-// so results are deterministic.  Out-of-range rows and chunks read zeros
+// 16 blocks are added by two DPP rotations inside each 16-lane row and
+// three v_permlane16/32_swap across rows; lanes 16v + j store the wave's
+// sum of row v for batch row j to LDS, and the workgroup adds them at the
+// end in wave order, so results are deterministic.  Out-of-range rows and chunks read zeros
 // through the buffer bound: a lane's offset past the workgroup's last row
 // or its matrix row stays past the bound for every row group it adds.
 constexpr int kXsMaxWaves = 16;
@@ -2172,7 +2172,8 @@ __global__ __launch_bounds__(kXsMaxWaves * kLanes) void gemm_raw_xs_kernel(
     const int n_rg = (int)(n_rg_all - rg0 < rg_per_block ? n_rg_all - rg0 : rg_per_block);
     const int64_t row_end = 4 * (rg0 + n_rg) < R ? 4 * (rg0 + n_rg) : R;
     const int64_t n_chunks = (C + kRawChunk - 1) / kRawChunk;
-    // the launcher keeps (R + 4 * (rg_per_block + PIPE)) * C below 2^32
+    // the launcher keeps R * C below 2^31 and every offset a workgroup forms,
+    // the row groups it loads past its end included, below 2^32
     const uint32_t bound = (uint32_t)(row_end * C);
     const Rsrc wsrc = rsrc(W, bound);
     const Rsrc xsrc = rsrc(x, (uint32_t)(NB * C * 2));
