@@ -109,7 +109,7 @@ def test_gemm_fused_vector_input_and_determinism(R):
                                          (37, 5136, 1), (9, 10256, 1), (70, 12000, 1),
                                          (17408, 5120, 8), (1001, 8176, 3), (403, 4112, 8),
                                          (40003, 2048, 6), (6, 8192, 2), (130, 8208, 8),
-                                         (37, 9008, 1)])
+                                         (37, 9008, 1), (257, 4096, 7), (64, 256, 4)])
 def test_gemm_raw_vs_float64(R, rows, cols, B):
     """The raw kernels: x held in registers for rows of up to 8192 columns
     at every B (one 256-column chunk per wave up to 16 chunks, then two:
